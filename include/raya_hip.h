@@ -1,0 +1,158 @@
+/*
+ * raya_hip.h: C ABI of libraya_hip.so, the MI355X (gfx950) backend for raya's
+ * block-local attention hot path and the encoder GEMMs.
+ *
+ * Plain pointers and sizes only.  Every entry point returns RAYA_OK (0) or one
+ * of the RAYA_ERR_* codes; details of the last failure on the calling thread
+ * are in raya_last_error().  Entry points never abort the process on bad
+ * arguments.
+ *
+ * Citations are to joaoajmatos/raya (Rust).
+ */
+#ifndef RAYA_HIP_H
+#define RAYA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error codes.  SHAPE, LENGTH and UNSUPPORTED are the three variants of
+ * KernelError (crates/raya-kernels/src/attention.rs:8-20); DEVICE carries a HIP
+ * runtime failure, which the reference (CPU only) never produces. */
+#define RAYA_OK 0
+#define RAYA_ERR_SHAPE 1
+#define RAYA_ERR_LENGTH 2
+#define RAYA_ERR_UNSUPPORTED 3
+#define RAYA_ERR_DEVICE 4
+
+/* Mask kinds: Mask::{Block3, Window64, Full, Sliding(w)}
+ * (crates/raya-kernels/src/attention.rs:22-35) plus BlockDiag(b), where a query
+ * in block i/b sees only the keys of its own block (no reference counterpart). */
+#define RAYA_MASK_BLOCK3 0
+#define RAYA_MASK_WINDOW64 1
+#define RAYA_MASK_FULL 2
+#define RAYA_MASK_SLIDING 3
+#define RAYA_MASK_BLOCKDIAG 4
+
+/* The reference's fixed block (attention.rs:4) and window (attention.rs:6). */
+#define RAYA_BLOCK 128
+#define RAYA_WINDOW 64
+
+/* AttnShape, attention.rs:72-84: buffers are [heads][seq][head_dim] f32. */
+typedef struct raya_attn_shape {
+    uint64_t heads;
+    uint64_t seq;
+    uint64_t head_dim;
+} raya_attn_shape;
+
+/* AttnParams, attention.rs:86-93, with the Mask enum flattened into
+ * (mask_kind, mask_arg): mask_arg is w for Sliding(w), b for BlockDiag(b) and
+ * ignored otherwise.  block must be RAYA_BLOCK, as the reference's validate
+ * requires (attention.rs:153-158). */
+typedef struct raya_attn_params {
+    int32_t mask_kind;
+    float scale;
+    uint64_t mask_arg;
+    uint64_t block;
+    uint64_t valid_len;
+} raya_attn_params;
+
+/* Details of the last failure on the calling thread.  For RAYA_ERR_LENGTH,
+ * buffer/got/expected are the fields of KernelError::Length; message is the
+ * error's Display text as the reference formats it. */
+typedef struct raya_error {
+    int32_t code;
+    char buffer[8];
+    uint64_t got;
+    uint64_t expected;
+    char message[512];
+} raya_error;
+
+const raya_error *raya_last_error(void);
+
+/* Stable names for bench output, like AttentionKernel::name (attention.rs:114)
+ * and GemmBackend::name (gemm.rs:3). */
+const char *raya_attention_name(void);
+const char *raya_gemm_name(void);
+
+/* AttentionKernel::attend (crates/raya-kernels/src/attention.rs:113-125) on
+ * host slices: validates like validate() (attention.rs:128-170) plus the
+ * HIP kernel's limits (head_dim <= 128), copies q/k/v to the current device,
+ * runs the fused kernel, copies out back and synchronises.  out is fully
+ * overwritten; rows >= valid_len are exact zeros. */
+int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params,
+                const float *q, size_t q_len, const float *k, size_t k_len,
+                const float *v, size_t v_len, float *out, size_t out_len);
+
+/* Row strides of one operand in floats.  All zero selects the dense
+ * [batch][heads][seq][head_dim] layout. */
+typedef struct raya_attn_layout {
+    int64_t batch_stride;
+    int64_t head_stride;
+    int64_t row_stride;
+} raya_attn_layout;
+
+/* A batch of sequences on the device: batch trait calls in one launch, each
+ * sequence with its own valid length.  No reference counterpart (the trait
+ * takes one sequence). */
+typedef struct raya_attn_batch {
+    uint64_t batch;
+    uint64_t heads;
+    uint64_t seq;
+    uint64_t head_dim;
+    int32_t mask_kind;
+    float scale;
+    uint64_t mask_arg;
+    uint64_t block;
+    raya_attn_layout q, k, v, out;
+} raya_attn_batch;
+
+/* Device pointers, asynchronous on `stream` (a hipStream_t; NULL is the null
+ * stream).  valid_len is a device array of batch int32 values; values outside
+ * [0, seq] are clamped into it.  Pointers must be 16-byte aligned and strides
+ * multiples of 4 floats. */
+int raya_attend_batched(const raya_attn_batch *desc, const int32_t *valid_len,
+                        const float *q, const float *k, const float *v, float *out,
+                        void *stream);
+
+/* GemmBackend::matmul_nt (crates/raya-kernels/src/gemm.rs:2-11) on host
+ * slices: out[m][n] = sum_t a[m][t] * b[n][t].  Length mismatches return
+ * RAYA_ERR_LENGTH with buffer "a", "b" or "out" and the reference's panic text
+ * ("a must be [m, k]", gemm.rs:23-25) as message; the caller re-raises them. */
+int raya_matmul_nt(float *out, size_t out_len, const float *a, size_t a_len,
+                   const float *b, size_t b_len, uint64_t m, uint64_t n, uint64_t k);
+
+/* GEMM epilogues: y = acc + bias; y = activation(y); out = y + residual.
+ * GELU is the exact erf form of ops::gelu (crates/raya-core/src/ops.rs:35-38),
+ * ReLU is ops::relu (ops.rs:41-43).  GEGLU follows the gated MLP of
+ * encoder::layer (crates/raya-core/src/encoder.rs:139-146): b has 2n rows and
+ * out[i][j] = gelu(y[i][j]) * y[i][n + j]. */
+#define RAYA_EPI_NONE 0
+#define RAYA_EPI_GELU 1
+#define RAYA_EPI_RELU 2
+#define RAYA_EPI_GEGLU 3
+
+typedef struct raya_gemm_epilogue {
+    int32_t activation;    /* RAYA_EPI_* */
+    int32_t reserved;      /* must be 0 */
+    const float *bias;     /* device [n] ([2n] for GEGLU) or NULL */
+    const float *residual; /* device [m][ldr] or NULL; may alias out when ldr == ldo */
+    int64_t ldr;
+} raya_gemm_epilogue;
+
+/* Device-pointer GEMM with a fused epilogue (ep may be NULL: plain product),
+ * asynchronous on `stream`.  Leading dimensions are in floats.  No reference
+ * counterpart: linear() (ops.rs:91-109) applies bias and activations on the
+ * host after matmul_nt. */
+int raya_matmul_nt_device(float *out, int64_t ldo, const float *a, int64_t lda, const float *b,
+                          int64_t ldb, uint64_t m, uint64_t n, uint64_t k,
+                          const raya_gemm_epilogue *ep, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,91 @@
+"""ctypes binding of libraya_hip.so (declarations of include/raya_hip.h).
+
+Loading the library does not touch the GPU; the first compute call does.
+A missing library is an error, never a silent fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libraya_hip.so")
+
+RAYA_OK, RAYA_ERR_SHAPE, RAYA_ERR_LENGTH, RAYA_ERR_UNSUPPORTED, RAYA_ERR_DEVICE = 0, 1, 2, 3, 4
+RAYA_MASK_BLOCK3, RAYA_MASK_WINDOW64, RAYA_MASK_FULL, RAYA_MASK_SLIDING, RAYA_MASK_BLOCKDIAG = range(5)
+RAYA_BLOCK, RAYA_WINDOW = 128, 64
+RAYA_EPI_NONE, RAYA_EPI_GELU, RAYA_EPI_RELU, RAYA_EPI_GEGLU = 0, 1, 2, 3
+
+
+class AttnShapeC(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint64), ("seq", ctypes.c_uint64), ("head_dim", ctypes.c_uint64)]
+
+
+class AttnParamsC(ctypes.Structure):
+    _fields_ = [("mask_kind", ctypes.c_int32), ("scale", ctypes.c_float),
+                ("mask_arg", ctypes.c_uint64), ("block", ctypes.c_uint64),
+                ("valid_len", ctypes.c_uint64)]
+
+
+class ErrorC(ctypes.Structure):
+    _fields_ = [("code", ctypes.c_int32), ("buffer", ctypes.c_char * 8),
+                ("got", ctypes.c_uint64), ("expected", ctypes.c_uint64),
+                ("message", ctypes.c_char * 512)]
+
+
+class AttnLayoutC(ctypes.Structure):
+    _fields_ = [("batch_stride", ctypes.c_int64), ("head_stride", ctypes.c_int64),
+                ("row_stride", ctypes.c_int64)]
+
+
+class AttnBatchC(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_uint64), ("heads", ctypes.c_uint64), ("seq", ctypes.c_uint64),
+                ("head_dim", ctypes.c_uint64), ("mask_kind", ctypes.c_int32),
+                ("scale", ctypes.c_float), ("mask_arg", ctypes.c_uint64),
+                ("block", ctypes.c_uint64), ("q", AttnLayoutC), ("k", AttnLayoutC),
+                ("v", AttnLayoutC), ("out", AttnLayoutC)]
+
+
+class GemmEpilogueC(ctypes.Structure):
+    _fields_ = [("activation", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64)]
+
+
+_fp = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u64, _i64 = ctypes.c_uint64, ctypes.c_int64
+
+# (name, restype, argtypes) of every exported function, in header order.
+SIGNATURES = [
+    ("raya_last_error", ctypes.POINTER(ErrorC), []),
+    ("raya_attention_name", ctypes.c_char_p, []),
+    ("raya_gemm_name", ctypes.c_char_p, []),
+    ("raya_attend", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
+                                   _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
+    ("raya_attend_batched", ctypes.c_int, [ctypes.POINTER(AttnBatchC), _vp, _vp, _vp, _vp, _vp, _vp]),
+    ("raya_matmul_nt", ctypes.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _u64, _u64, _u64]),
+    ("raya_matmul_nt_device", ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _u64, _u64, _u64,
+                                             ctypes.POINTER(GemmEpilogueC), _vp]),
+]
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build the HIP backend with `python -m raya_amd.build`")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> ErrorC:
+    return lib().raya_last_error().contents

@@ -1,0 +1,297 @@
+"""Host-side mirror of the reference's `raya-kernels` interface over libraya_hip.
+
+The names, argument meanings and error behaviour follow
+crates/raya-kernels/src/attention.rs and gemm.rs:
+
+* ``Mask``, ``AttnShape``, ``AttnParams`` and ``KernelError`` (with ``Shape``,
+  ``Length`` and ``Unsupported`` variants) as in attention.rs:8-106;
+* ``AttentionKernel`` with ``name()`` and
+  ``attend(shape, params, q, k, v, out)`` (attention.rs:113-125);
+* ``GemmBackend`` with ``name()`` and ``matmul_nt(out, a, b, m, n, k)``
+  (gemm.rs:2-11), which panics (raises ``AssertionError``) on bad lengths.
+
+``HipAttention`` and ``HipGemm`` run on the GPU through the C ABI; there is no
+CPU path in this package.  Device-resident entry points (``attend_batched``,
+``matmul_nt_device``) take torch tensors already in HBM.
+"""
+from __future__ import annotations
+
+import abc
+import ctypes
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _capi as C
+
+BLOCK = C.RAYA_BLOCK    # attention.rs:4
+WINDOW = C.RAYA_WINDOW  # attention.rs:6
+
+
+class KernelError(Exception):
+    """KernelError (attention.rs:8-20)."""
+
+
+class ShapeError(KernelError):
+    """KernelError::Shape."""
+
+
+class LengthError(KernelError):
+    """KernelError::Length { name, got, expected }."""
+
+    def __init__(self, message: str, name: str, got: int, expected: int):
+        super().__init__(message)
+        self.name, self.got, self.expected = name, got, expected
+
+
+class UnsupportedError(KernelError):
+    """KernelError::Unsupported."""
+
+
+class DeviceError(KernelError):
+    """A HIP runtime failure (no counterpart in the CPU-only reference)."""
+
+
+def _raise_last(rc: int):
+    e = C.last_error()
+    msg = e.message.decode()
+    if rc == C.RAYA_ERR_SHAPE:
+        raise ShapeError(msg)
+    if rc == C.RAYA_ERR_LENGTH:
+        raise LengthError(msg, e.buffer.decode(), e.got, e.expected)
+    if rc == C.RAYA_ERR_UNSUPPORTED:
+        raise UnsupportedError(msg)
+    raise DeviceError(msg)
+
+
+@dataclass(frozen=True)
+class Mask:
+    """Mask (attention.rs:22-35) plus BlockDiag(b): query block i/b sees only its own block."""
+
+    kind: int
+    arg: int = 0
+
+    @staticmethod
+    def sliding(w: int) -> "Mask":
+        return Mask(C.RAYA_MASK_SLIDING, w)
+
+    @staticmethod
+    def block_diag(b: int) -> "Mask":
+        return Mask(C.RAYA_MASK_BLOCKDIAG, b)
+
+    def name(self) -> str:
+        return {C.RAYA_MASK_BLOCK3: "block3", C.RAYA_MASK_WINDOW64: "window64",
+                C.RAYA_MASK_FULL: "full", C.RAYA_MASK_SLIDING: "sliding",
+                C.RAYA_MASK_BLOCKDIAG: "block_diag"}[self.kind]
+
+    def key_range(self, i: int, valid_len: int) -> range:
+        """Keys row i may attend, clipped to valid_len (attention.rs:48-59)."""
+        if self.kind == C.RAYA_MASK_BLOCK3:
+            b = i // BLOCK
+            lo, hi = max(b - 1, 0) * BLOCK, (b + 2) * BLOCK
+        elif self.kind == C.RAYA_MASK_WINDOW64:
+            lo, hi = max(i - WINDOW, 0), i + WINDOW + 1
+        elif self.kind == C.RAYA_MASK_FULL:
+            lo, hi = 0, valid_len
+        elif self.kind == C.RAYA_MASK_SLIDING:
+            lo, hi = max(i - self.arg, 0), i + self.arg + 1
+        else:
+            b = i // self.arg
+            lo, hi = b * self.arg, (b + 1) * self.arg
+        return range(min(lo, valid_len), min(hi, valid_len))
+
+    def allows(self, i: int, j: int) -> bool:
+        """Whether query i may attend key j, ignoring valid_len (attention.rs:62-69)."""
+        if self.kind == C.RAYA_MASK_BLOCK3:
+            return abs(i // BLOCK - j // BLOCK) <= 1
+        if self.kind == C.RAYA_MASK_WINDOW64:
+            return abs(i - j) <= WINDOW
+        if self.kind == C.RAYA_MASK_FULL:
+            return True
+        if self.kind == C.RAYA_MASK_SLIDING:
+            return abs(i - j) <= self.arg
+        return i // self.arg == j // self.arg
+
+
+Mask.BLOCK3 = Mask(C.RAYA_MASK_BLOCK3)
+Mask.WINDOW64 = Mask(C.RAYA_MASK_WINDOW64)
+Mask.FULL = Mask(C.RAYA_MASK_FULL)
+
+
+@dataclass(frozen=True)
+class AttnShape:
+    """AttnShape (attention.rs:72-84): buffers are [heads][seq][head_dim]."""
+
+    heads: int
+    seq: int
+    head_dim: int
+
+    def numel(self) -> int:
+        return self.heads * self.seq * self.head_dim
+
+
+@dataclass(frozen=True)
+class AttnParams:
+    """AttnParams (attention.rs:86-106)."""
+
+    mask: Mask
+    block: int
+    valid_len: int
+    scale: float
+
+    @staticmethod
+    def new(mask: Mask, valid_len: int, head_dim: int) -> "AttnParams":
+        """Block 128 and scale 1/sqrt(head_dim) computed in f32 (attention.rs:98-105)."""
+        scale = np.float32(1.0) / np.sqrt(np.float32(head_dim))
+        return AttnParams(mask, BLOCK, valid_len, float(scale))
+
+    def replace(self, **kw) -> "AttnParams":
+        d = dict(mask=self.mask, block=self.block, valid_len=self.valid_len, scale=self.scale)
+        d.update(kw)
+        return AttnParams(**d)
+
+
+class AttentionKernel(abc.ABC):
+    """AttentionKernel (attention.rs:113-125)."""
+
+    @abc.abstractmethod
+    def name(self) -> str: ...
+
+    @abc.abstractmethod
+    def attend(self, shape: AttnShape, params: AttnParams, q, k, v, out) -> None: ...
+
+
+class GemmBackend(abc.ABC):
+    """GemmBackend (gemm.rs:2-11)."""
+
+    @abc.abstractmethod
+    def name(self) -> str: ...
+
+    @abc.abstractmethod
+    def matmul_nt(self, out, a, b, m: int, n: int, k: int) -> None: ...
+
+
+def _host_f32(x, name: str):
+    """(pointer, length) of a contiguous float32 host buffer."""
+    if not isinstance(x, np.ndarray) or x.dtype != np.float32 or not x.flags.c_contiguous:
+        raise TypeError(f"`{name}` must be a contiguous numpy float32 array")
+    return ctypes.c_void_p(x.ctypes.data), x.size
+
+
+def _dev_ptr(t, name: str) -> ctypes.c_void_p:
+    import torch
+
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"`{name}` must be a torch tensor on the GPU")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream_ptr(stream) -> ctypes.c_void_p:
+    import torch
+
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+class HipAttention(AttentionKernel):
+    """The fused HIP block-local attention kernel (gfx950) as an AttentionKernel."""
+
+    def name(self) -> str:
+        return C.lib().raya_attention_name().decode()
+
+    def attend(self, shape: AttnShape, params: AttnParams, q, k, v, out) -> None:
+        """Host slices in, out overwritten; errors raise KernelError subclasses."""
+        (qp, ql), (kp, kl), (vp, vl), (op, ol) = (
+            _host_f32(q, "q"), _host_f32(k, "k"), _host_f32(v, "v"), _host_f32(out, "out"))
+        if not out.flags.writeable:
+            raise TypeError("`out` must be writeable")
+        s = C.AttnShapeC(shape.heads, shape.seq, shape.head_dim)
+        p = C.AttnParamsC(params.mask.kind, params.scale, params.mask.arg, params.block,
+                          params.valid_len)
+        rc = C.lib().raya_attend(ctypes.byref(s), ctypes.byref(p), qp, ql, kp, kl, vp, vl, op, ol)
+        if rc:
+            _raise_last(rc)
+
+    def attend_batched(self, q, k, v, out, valid_len, mask: Mask, scale: float | None = None,
+                       block: int = BLOCK, layouts=None, stream=None) -> None:
+        """Batched device path: q/k/v/out are GPU tensors viewed as
+        [batch][heads][seq][head_dim] (or with explicit ``layouts``: a dict of
+        name -> (batch_stride, head_stride, row_stride) in floats, plus
+        ``shape`` = (batch, heads, seq, head_dim)); valid_len is a GPU int32
+        tensor [batch].  Asynchronous on ``stream`` (torch's current stream by
+        default)."""
+        import torch
+
+        if layouts is None:
+            if q.dim() != 4:
+                raise ShapeError("invalid shape: q must be [batch, heads, seq, head_dim]")
+            b, h, s_, d = q.shape
+            for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+                if tuple(t.shape) != (b, h, s_, d) or not t.is_contiguous():
+                    raise ShapeError(f"invalid shape: `{name}` must be a contiguous [b, h, s, d] tensor")
+            lay = {n: (0, 0, 0) for n in ("q", "k", "v", "out")}
+        else:
+            b, h, s_, d = layouts["shape"]
+            lay = {n: layouts[n] for n in ("q", "k", "v", "out")}
+        for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+            if t.dtype != torch.float32:
+                raise TypeError(f"`{name}` must be float32")
+        if valid_len.dtype != torch.int32 or not valid_len.is_cuda or valid_len.numel() != b:
+            raise ShapeError("invalid shape: valid_len must be a GPU int32 tensor of batch entries")
+        if scale is None:
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+        desc = C.AttnBatchC(b, h, s_, d, mask.kind, scale, mask.arg, block,
+                            C.AttnLayoutC(*lay["q"]), C.AttnLayoutC(*lay["k"]),
+                            C.AttnLayoutC(*lay["v"]), C.AttnLayoutC(*lay["out"]))
+        rc = C.lib().raya_attend_batched(ctypes.byref(desc), _dev_ptr(valid_len, "valid_len"),
+                                         _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"),
+                                         _dev_ptr(out, "out"), _stream_ptr(stream))
+        if rc:
+            _raise_last(rc)
+
+
+class HipGemm(GemmBackend):
+    """The MFMA fp32 GEMM (gfx950) as a GemmBackend."""
+
+    def name(self) -> str:
+        return C.lib().raya_gemm_name().decode()
+
+    def matmul_nt(self, out, a, b, m: int, n: int, k: int) -> None:
+        (op, ol), (ap, al), (bp, bl) = _host_f32(out, "out"), _host_f32(a, "a"), _host_f32(b, "b")
+        rc = C.lib().raya_matmul_nt(op, ol, ap, al, bp, bl, m, n, k)
+        if rc == C.RAYA_ERR_LENGTH:
+            # Reference::matmul_nt panics on a length mismatch (gemm.rs:23-25).
+            raise AssertionError(C.last_error().message.decode())
+        if rc:
+            _raise_last(rc)
+
+    def matmul_nt_device(self, out, a, b, *, bias=None, activation: int = C.RAYA_EPI_NONE,
+                         residual=None, stream=None) -> None:
+        """out[m, n] = act(a[m, k] @ b[n, k]^T + bias) + residual on GPU tensors.
+        For GEGLU, b is [2n, k] and bias [2n].  Row strides are taken from the
+        tensors (last dimension must be contiguous)."""
+        m, k = a.shape
+        n = out.shape[1]
+        for name, t in (("out", out), ("a", a), ("b", b)):
+            if t.dim() != 2 or t.stride(1) != 1:
+                raise ShapeError(f"invalid shape: `{name}` must be 2-D with contiguous rows")
+        rows_b = 2 * n if activation == C.RAYA_EPI_GEGLU else n
+        if tuple(b.shape) != (rows_b, k) or out.shape[0] != m:
+            raise ShapeError("invalid shape: operands do not agree")
+        ep = C.GemmEpilogueC(activation, 0,
+                             ctypes.c_void_p(bias.data_ptr()) if bias is not None else None,
+                             ctypes.c_void_p(residual.data_ptr()) if residual is not None else None,
+                             residual.stride(0) if residual is not None else 0)
+        rc = C.lib().raya_matmul_nt_device(_dev_ptr(out, "out"), out.stride(0), _dev_ptr(a, "a"),
+                                           a.stride(0), _dev_ptr(b, "b"), b.stride(0), m, n, k,
+                                           ctypes.byref(ep), _stream_ptr(stream))
+        if rc:
+            _raise_last(rc)
+
+
+def default_scale(head_dim: int) -> float:
+    return float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+
+
+assert math.isclose(default_scale(64), 0.125)

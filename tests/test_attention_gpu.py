@@ -1,0 +1,248 @@
+"""Parity of the HIP attention kernel with the CPU oracle, through the C ABI.
+
+Bar: max-abs 1e-5 and rel-L2 1e-5 against the restated Naive kernel on the
+same inputs (the tighter of the reference's 1e-5 Tiled-vs-Naive bar and the
+target's max-abs 1e-4 / rel-L2 1e-5); padded rows exactly zero; masks exact.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+from safetensors.numpy import load_file
+
+import oracle
+import raya_amd as R
+from raya_amd import synth
+from tests.conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 1e-5
+REL_L2 = 1e-5
+
+MASKS = {
+    "block3": (R.Mask.BLOCK3, oracle.MASK_BLOCK3, 128, 0),
+    "window64": (R.Mask.WINDOW64, oracle.MASK_WINDOW64, 128, 0),
+    "full": (R.Mask.FULL, oracle.MASK_FULL, 128, 0),
+    "sliding8": (R.Mask.sliding(8), oracle.MASK_SLIDING, 128, 8),
+    "sliding64": (R.Mask.sliding(64), oracle.MASK_SLIDING, 128, 64),
+    "block_diag64": (R.Mask.block_diag(64), oracle.MASK_BLOCKDIAG, 64, 0),
+    "block_diag128": (R.Mask.block_diag(128), oracle.MASK_BLOCKDIAG, 128, 0),
+}
+
+
+def check_close(got, want, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    diff = np.abs(got - want)
+    mx = float(diff.max()) if diff.size else 0.0
+    denom = float(np.sqrt((want ** 2).sum()))
+    rel = float(np.sqrt((diff ** 2).sum())) / denom if denom > 0 else mx
+    assert mx < MAX_ABS and rel < REL_L2, f"{what}: max-abs {mx:.3g}, rel-L2 {rel:.3g}"
+
+
+def run_hip(kernel, q, k, v, mask, valid, fill=7.0):
+    h, s, d = q.shape
+    out = np.full(q.shape, fill, np.float32)
+    kernel.attend(R.AttnShape(h, s, d), R.AttnParams.new(mask, valid, d),
+                  q.ravel(), k.ravel(), v.ravel(), out.reshape(-1))
+    return out
+
+
+def oracle_naive(q, k, v, okind, valid, block, window):
+    d = q.shape[2]
+    return oracle.naive_attend(q, k, v, okind, valid, R.kernels.default_scale(d),
+                               block=block, window=window)
+
+
+def test_golden_block_local_L256(hip_attention):
+    """goldens.rs:35-80 through the HIP kernel: within 1e-5 of both golden outputs."""
+    d = os.path.join(GOLDEN, "block_local_L256")
+    meta = json.load(open(os.path.join(d, "meta.json")))
+    t = load_file(os.path.join(d, "tensors.safetensors"))
+    q, k, v = t["q"][0], t["k"][0], t["v"][0]
+    got = run_hip(hip_attention, q, k, v, R.Mask.BLOCK3, meta["length"])
+    for which in ("reference", "kernel"):
+        assert np.abs(got - t[which][0]).max() < meta["tolerance"]
+    check_close(got, oracle_naive(q, k, v, oracle.MASK_BLOCK3, 256, 128, 0), "golden inputs")
+
+
+@pytest.mark.parametrize("name", list(MASKS))
+def test_matches_naive_at_edge_lengths(hip_attention, name):
+    """oracle.rs / equivalence.rs lengths, padded tails and head counts, for every mask."""
+    mask, okind, block, window = MASKS[name]
+    cases = [(s, s, 3) for s in (1, 7, 127, 128, 129, 257)]
+    cases += [(1000, 1000, 2), (2048, 2048, 2)]
+    cases += [(300, 263, 2), (1000, 963, 2), (256, 1, 2), (256, 0, 2), (129, 128, 2), (257, 220, 1)]
+    for seq, valid, heads in cases:
+        q, k, v = oracle.qkv(heads, seq, 64, 100 + seq)
+        got = run_hip(hip_attention, q, k, v, mask, valid)
+        want = oracle_naive(q, k, v, okind, valid, block, window)
+        check_close(got, want, f"{name} seq {seq} valid {valid}")
+        assert (got[:, valid:, :] == 0).all()
+
+
+@pytest.mark.parametrize("d", [8, 16, 24, 40, 64, 72, 96, 128])
+def test_matches_naive_for_every_head_dim(hip_attention, d):
+    """equivalence.rs:77-112 and dispatch.rs head dims (8..128)."""
+    for name in ("block3", "window64", "block_diag64"):
+        mask, okind, block, window = MASKS[name]
+        for seq, valid in ((300, 300), (200, 130)):
+            q, k, v = oracle.qkv(2, seq, d, 3)
+            got = run_hip(hip_attention, q, k, v, mask, valid)
+            check_close(got, oracle_naive(q, k, v, okind, valid, block, window), f"{name} d{d}")
+
+
+def test_sixteen_heads_bench_shape(hip_attention):
+    """equivalence.rs:77-91: 16 heads x 512, and the bench's own inputs (seed 42)."""
+    for name in ("block3", "window64"):
+        mask, okind, block, window = MASKS[name]
+        q, k, v = oracle.qkv(16, 512, 64, 42)
+        got = run_hip(hip_attention, q, k, v, mask, 512)
+        check_close(got, oracle_naive(q, k, v, okind, 512, block, window), name)
+
+
+@pytest.mark.parametrize("name", ["block3", "window64", "block_diag64"])
+def test_masks_are_exact(hip_attention, name):
+    """masking.rs:20-61 with V one-hot on key j."""
+    mask, okind, block, window = MASKS[name]
+    seq, d = 300, 8
+    q = oracle.rand_vec(seq * d, 5).reshape(1, seq, d)
+    k = oracle.rand_vec(seq * d, 6).reshape(1, seq, d)
+    for j in (0, 1, 63, 64, 65, 127, 128, 129, 191, 255, 256, 299):
+        v = np.zeros((1, seq, d), np.float32)
+        v[0, j, 0] = 1.0
+        out = run_hip(hip_attention, q, k, v, mask, seq)
+        for i in range(seq):
+            assert (out[0, i, 0] > 0) == mask.allows(i, j), (i, j)
+
+
+def test_padding_rows_are_exact_zeros_and_finite(hip_attention):
+    """masking.rs:63-91: rows >= valid are exact zeros even when out held garbage."""
+    q, k, v = oracle.qkv(2, 200, 16, 9)
+    for name in ("block3", "window64", "full", "block_diag64"):
+        mask = MASKS[name][0]
+        for valid in (0, 1, 150):
+            out = run_hip(hip_attention, q, k, v, mask, valid, fill=np.nan)
+            assert (out[:, valid:, :] == 0).all() and np.isfinite(out).all()
+
+
+def test_extreme_logits_are_stable(hip_attention):
+    """masking.rs:93-125: q, k x400 (scores ~1e4) stay finite and match the oracle."""
+    q, k, v = oracle.qkv(2, 300, 64, 21)
+    q, k = q * 400.0, k * 400.0
+    for name in ("block3", "window64"):
+        mask, okind, block, window = MASKS[name]
+        got = run_hip(hip_attention, q, k, v, mask, 300)
+        assert np.isfinite(got).all()
+        check_close(got, oracle_naive(q, k, v, okind, 300, block, window), name)
+
+
+def test_single_valid_row_and_nothing_valid(hip_attention):
+    """masks_edges.rs:64-107."""
+    q = oracle.lcg_fill(40, 31).reshape(1, 5, 8)
+    k = oracle.lcg_fill(40, 32).reshape(1, 5, 8)
+    v = oracle.lcg_fill(40, 33).reshape(1, 5, 8)
+    for mask in (R.Mask.FULL, R.Mask.sliding(2)):
+        out = run_hip(hip_attention, q, k, v, mask, 1)
+        assert np.abs(out[0, 0] - v[0, 0]).max() < 1e-6 and (out[0, 1:] == 0).all()
+        out = run_hip(hip_attention, q, k, v, mask, 0)
+        assert (out == 0).all()
+
+
+def _dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+def test_batched_device_path_dense_and_strided(hip_attention):
+    """One launch over sequences with their own valid lengths; packed [B, L, 3, H, D] input."""
+    b, h, s, d = 3, 2, 300, 64
+    valid = np.array([300, 217, 0], np.int32)
+    q, k, v = (synth.normal(7 + i, b * h * s * d).reshape(b, h, s, d) for i in range(3))
+    for name in ("block3", "window64", "block_diag64", "full"):
+        mask, okind, block, window = MASKS[name]
+        want = oracle.naive_attend_batched(q, k, v, okind, valid, R.kernels.default_scale(d),
+                                           block=block, window=window)
+        out = torch.full((b, h, s, d), 5.0, device="cuda")
+        hip_attention.attend_batched(_dev(q), _dev(k), _dev(v), out, _dev(valid), mask)
+        torch.cuda.synchronize()
+        check_close(out.cpu().numpy(), want, f"dense {name}")
+        # Packed projection layout [B, L, 3, H, D] in, token-major context [B, L, H, D] out.
+        packed = np.stack([q, k, v], axis=2).transpose(0, 3, 2, 1, 4).copy()  # b, s, 3, h, d
+        pk = _dev(packed)
+        ctx = torch.full((b, s, h, d), 5.0, device="cuda")
+        qkv_lay = lambda which: (s * 3 * h * d, d, 3 * h * d)
+        lay = {"shape": (b, h, s, d), "q": qkv_lay(0), "k": qkv_lay(1), "v": qkv_lay(2),
+               "out": (s * h * d, d, h * d)}
+        hip_attention.attend_batched(pk[:, :, 0], pk[:, :, 1], pk[:, :, 2], ctx, _dev(valid), mask,
+                                     layouts=lay)
+        torch.cuda.synchronize()
+        check_close(ctx.cpu().numpy().transpose(0, 2, 1, 3), want, f"strided {name}")
+
+
+def test_workload_block_diag64_b1_l512(hip_attention):
+    """B=1, H=12, D=64, L=512, BlockDiag(64), N(0,1) inputs, no padding."""
+    h, s, d = 12, 512, 64
+    q, k, v = (synth.normal(synth.workload_seed(1, i), h * s * d).reshape(h, s, d) for i in range(3))
+    got = run_hip(hip_attention, q, k, v, R.Mask.block_diag(64), s)
+    check_close(got, oracle_naive(q, k, v, oracle.MASK_BLOCKDIAG, s, 64, 0), "b1 l512")
+
+
+def test_workload_block_diag64_l2048_padded(hip_attention):
+    """H=12, D=64, L=2048, BlockDiag(64), valid ~ U[512, 2048]: 4 sequences vs the oracle."""
+    b, h, s, d = 4, 12, 2048, 64
+    n = b * h * s * d
+    q, k, v = (synth.normal(synth.workload_seed(2, i), n).reshape(b, h, s, d) for i in range(3))
+    valid = synth.integers(synth.workload_seed(2, 3), b, s // 4, s).astype(np.int32)
+    out = torch.empty((b, h, s, d), device="cuda")
+    hip_attention.attend_batched(_dev(q), _dev(k), _dev(v), out, _dev(valid), R.Mask.block_diag(64))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    want = oracle.naive_attend_batched(q, k, v, oracle.MASK_BLOCKDIAG, valid, 0.125, block=64)
+    for i in range(b):
+        check_close(got[i, :, : valid[i]], want[i, :, : valid[i]], f"seq {i}")
+        assert (got[i, :, valid[i]:] == 0).all()
+
+
+def test_workload_block_diag128_l16384_outliers(hip_attention):
+    """H=12, D=64, L=16384, BlockDiag(128), 1% outliers x20, one sequence vs the oracle."""
+    h, s, d = 12, 16384, 64
+    n = h * s * d
+    q, k, v = (synth.with_outliers(synth.normal(synth.workload_seed(5, i), n),
+                                   synth.workload_seed(5, 4) + 10 * i).reshape(h, s, d)
+               for i in range(3))
+    valid = int(synth.integers(synth.workload_seed(5, 3), 1, s // 2, s)[0])
+    got = run_hip(hip_attention, q, k, v, R.Mask.block_diag(128), valid)
+    want, _ = oracle.tiled_attend_batched(q[None], k[None], v[None], oracle.MASK_BLOCKDIAG, [valid],
+                                          0.125, block=128, threads=min(16, os.cpu_count() or 1))
+    check_close(got[:, :valid], want[0, :, :valid], "l16384")
+    assert (got[:, valid:] == 0).all()
+
+
+def test_full_size_properties_b32_l2048(hip_attention):
+    """At the full B=32 workload: with V = 1 every valid row is exactly a convex combination
+    summing to 1; linearity in V holds; padded rows are zero."""
+    b, h, s, d = 32, 12, 2048, 64
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    q = torch.randn((b, h, s, d), device="cuda", generator=g)
+    k = torch.randn((b, h, s, d), device="cuda", generator=g)
+    valid_np = synth.integers(synth.workload_seed(2, 3), b, s // 4, s).astype(np.int32)
+    valid = _dev(valid_np)
+    ones = torch.ones((b, h, s, d), device="cuda")
+    out = torch.empty_like(q)
+    mask = R.Mask.block_diag(64)
+    hip_attention.attend_batched(q, k, ones, out, valid, mask)
+    torch.cuda.synchronize()
+    rows = torch.arange(s, device="cuda")[None, None, :, None] < valid.long()[:, None, None, None]
+    assert torch.all(torch.where(rows, (out - 1).abs() < 1e-5, out == 0))
+    v1 = torch.randn((b, h, s, d), device="cuda", generator=g)
+    v2 = torch.randn((b, h, s, d), device="cuda", generator=g)
+    o1, o2, o12 = torch.empty_like(q), torch.empty_like(q), torch.empty_like(q)
+    hip_attention.attend_batched(q, k, v1, o1, valid, mask)
+    hip_attention.attend_batched(q, k, v2, o2, valid, mask)
+    hip_attention.attend_batched(q, k, v1 + v2, o12, valid, mask)
+    torch.cuda.synchronize()
+    assert float((o12 - o1 - o2).abs().max()) < 2e-5
+    assert bool(torch.all(torch.where(rows, True, o12 == 0)))

@@ -1,0 +1,123 @@
+"""The C ABI on the CPU: the library loads, exports what include/*.h declares, and
+rejects bad arguments with the reference's error variants before any GPU work."""
+import ctypes
+import glob
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+import raya_amd as R
+from raya_amd import _capi as C
+from tests.conftest import ROOT
+
+
+def declared_functions():
+    names = []
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^[a-z_][\w\s\*]*?\b(raya_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_function():
+    names = declared_functions()
+    assert "raya_attend" in names and "raya_matmul_nt_device" in names
+    lib = C.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(n for n, _, _ in C.SIGNATURES) == names
+
+
+def test_names():
+    assert R.HipAttention().name() == "hip-gfx950"
+    assert R.HipGemm().name() == "hip-gfx950-mfma"
+
+
+def _ok(shape):
+    return np.zeros(shape.numel(), np.float32)
+
+
+def test_bad_arguments_are_errors_not_panics():
+    """crates/raya-kernels/tests/oracle.rs:34-78, through the C ABI."""
+    k = R.HipAttention()
+    shape = R.AttnShape(1, 4, 8)
+    ok, out = _ok(shape), _ok(shape)
+    p = R.AttnParams.new(R.Mask.BLOCK3, 4, 8)
+    with pytest.raises(R.LengthError) as e:
+        k.attend(shape, p, np.zeros(3, np.float32), ok, ok, out)
+    assert e.value.name == "q" and e.value.got == 3 and e.value.expected == 32
+    assert str(e.value) == "buffer `q` has length 3, expected 32"
+    with pytest.raises(R.LengthError) as e:
+        k.attend(shape, p, ok, ok, ok, np.zeros(3, np.float32))
+    assert e.value.name == "out"
+    bad = R.AttnShape(1, 4, 12)
+    buf = _ok(bad)
+    with pytest.raises(R.ShapeError):
+        k.attend(bad, p, buf, buf, buf, _ok(bad))
+    with pytest.raises(R.ShapeError):
+        k.attend(shape, p.replace(valid_len=5), ok, ok, ok, out)
+    with pytest.raises(R.UnsupportedError):
+        k.attend(shape, p.replace(block=64), ok, ok, ok, out)
+    with pytest.raises(R.ShapeError):
+        k.attend(R.AttnShape(0, 4, 8), p, ok[:0], ok[:0], ok[:0], out[:0])
+
+
+def test_hip_limits_are_unsupported_not_wrong():
+    k = R.HipAttention()
+    shape = R.AttnShape(1, 2, 136)
+    buf = _ok(shape)
+    with pytest.raises(R.UnsupportedError):
+        k.attend(shape, R.AttnParams.new(R.Mask.WINDOW64, 2, 136), buf, buf, buf, _ok(shape))
+    with pytest.raises(R.ShapeError):
+        k.attend(R.AttnShape(1, 4, 8), R.AttnParams.new(R.Mask.block_diag(0), 4, 8),
+                 *(_ok(R.AttnShape(1, 4, 8)) for _ in range(4)))
+
+
+def test_empty_sequence_is_a_no_op():
+    k = R.HipAttention()
+    e = np.zeros(0, np.float32)
+    k.attend(R.AttnShape(2, 0, 8), R.AttnParams.new(R.Mask.BLOCK3, 0, 8), e, e, e, e)
+
+
+def test_gemm_length_checks_panic_like_the_reference():
+    """gemm_reference.rs:24-31, gemm_edges.rs:4-24."""
+    g = R.HipGemm()
+    with pytest.raises(AssertionError, match="a must be"):
+        g.matmul_nt(np.zeros(1, np.float32), np.ones(1, np.float32), np.ones(2, np.float32), 1, 1, 2)
+    with pytest.raises(AssertionError, match="b must be"):
+        g.matmul_nt(np.zeros(1, np.float32), np.ones(2, np.float32), np.ones(1, np.float32), 1, 1, 2)
+    with pytest.raises(AssertionError, match="out must be"):
+        g.matmul_nt(np.zeros(2, np.float32), np.ones(2, np.float32), np.ones(2, np.float32), 1, 1, 2)
+    none = np.zeros(0, np.float32)
+    g.matmul_nt(none, none, np.ones(2, np.float32), 0, 1, 2)
+    g.matmul_nt(none, np.ones(2, np.float32), none, 1, 0, 2)
+    g.matmul_nt(none, none, none, 0, 0, 0)
+
+
+def test_gemm_empty_k_needs_no_gpu():
+    out = np.full(6, 5.0, np.float32)
+    R.HipGemm().matmul_nt(out, np.zeros(0, np.float32), np.zeros(0, np.float32), 2, 3, 0)
+    assert (out == 0).all()
+
+
+@pytest.mark.parametrize("mask,okind,block,window", [
+    (R.Mask.BLOCK3, oracle.MASK_BLOCK3, 128, 0), (R.Mask.WINDOW64, oracle.MASK_WINDOW64, 128, 0),
+    (R.Mask.FULL, oracle.MASK_FULL, 128, 0), (R.Mask.sliding(9), oracle.MASK_SLIDING, 128, 9),
+    (R.Mask.block_diag(64), oracle.MASK_BLOCKDIAG, 64, 0)])
+def test_host_mask_mirror_agrees_with_the_oracle(mask, okind, block, window):
+    for valid in (0, 1, 130, 300):
+        for i in range(0, 300, 7):
+            r = mask.key_range(i, valid)
+            assert (r.start, r.stop) == oracle.key_range(okind, i, valid, block=block, window=window)
+            for j in range(0, 300, 13):
+                assert mask.allows(i, j) == oracle.allows(okind, i, j, block=block, window=window)
+
+
+def test_default_params():
+    p = R.AttnParams.new(R.Mask.BLOCK3, 10, 40)
+    assert p.block == 128 and p.valid_len == 10
+    assert np.float32(p.scale) == np.float32(1.0) / np.sqrt(np.float32(40))

@@ -1,0 +1,95 @@
+"""Parity of the MFMA GEMM with the oracle's Reference::matmul_nt, through the C ABI.
+
+Bar (specs/009-gemm-backend-comparison/spec.md:24): every element within
+2 * k * 2^-24 * sum_t |a_t b_t| of the sequential f32 result; hand values and
+NaN/Inf propagation exact, as the reference's tests pin them.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import raya_amd as R
+from raya_amd import _capi as C
+
+pytestmark = pytest.mark.gpu
+
+
+def bound(a, b):
+    k = a.shape[1]
+    return 2 * k * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64).T)
+
+
+def run(gemm, a, b):
+    m, k = a.shape
+    n = b.shape[0]
+    out = np.full((m, n), 3.0, np.float32)
+    gemm.matmul_nt(out.reshape(-1), a.reshape(-1), b.reshape(-1), m, n, k)
+    return out
+
+
+def test_hand_values(hip_gemm):
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[1, 0, -1], [2, 1, 0.5]], np.float32)
+    assert np.array_equal(run(hip_gemm, a, b), np.array([[-2, 5.5], [-2, 16]], np.float32))
+
+
+def test_empty_k_overwrites_with_zeros(hip_gemm):
+    out = np.full(6, 5.0, np.float32)
+    hip_gemm.matmul_nt(out, np.zeros(0, np.float32), np.zeros(0, np.float32), 2, 3, 0)
+    assert (out == 0).all()
+
+
+def test_nan_and_inf_propagate(hip_gemm):
+    assert np.isnan(run(hip_gemm, np.array([[np.nan, 1]], np.float32), np.ones((2, 2), np.float32))).all()
+    out = run(hip_gemm, np.array([[np.inf, 1]], np.float32), np.array([[1, 0], [-1, 0]], np.float32))
+    assert out[0, 0] == np.inf and out[0, 1] == -np.inf
+    out = run(hip_gemm, np.array([[np.inf, 1]], np.float32), np.array([[0, 1], [1, 1]], np.float32))
+    assert np.isnan(out[0, 0]) and out[0, 1] == np.inf
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (3, 5, 7), (17, 9, 33), (64, 64, 64), (130, 31, 257),
+                                   (256, 2304, 768), (300, 768, 3072), (129, 6144, 768)])
+def test_within_the_reordering_bound(hip_gemm, m, n, k):
+    rng = np.random.default_rng(m * 7 + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (0.02 * rng.standard_normal((n, k))).astype(np.float32)
+    got = run(hip_gemm, a, b).astype(np.float64)
+    want = oracle.matmul_nt(a, b, threads=8).astype(np.float64)
+    assert (np.abs(got - want) <= bound(a, b)).all()
+
+
+def _dev(x):
+    return torch.from_numpy(np.ascontiguousarray(x)).cuda()
+
+
+@pytest.mark.parametrize("act", ["none", "gelu", "relu", "geglu"])
+@pytest.mark.parametrize("residual", [False, True])
+def test_device_epilogues(hip_gemm, act, residual):
+    """bias + activation (+ residual) against the oracle's matmul_nt and scalar ops."""
+    rng = np.random.default_rng(5)
+    m, n, k = 200, 96, 136
+    rows_b = 2 * n if act == "geglu" else n
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = (0.1 * rng.standard_normal((rows_b, k))).astype(np.float32)
+    bias = rng.standard_normal(rows_b).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    y = oracle.matmul_nt(a, b) + bias
+    if act == "gelu":
+        want = oracle.gelu_array(y)
+    elif act == "relu":
+        want = np.maximum(y, 0)
+    elif act == "geglu":
+        want = oracle.gelu_array(y[:, :n]) * y[:, n:]
+    else:
+        want = y
+    if residual:
+        want = want + res
+    code = {"none": C.RAYA_EPI_NONE, "gelu": C.RAYA_EPI_GELU, "relu": C.RAYA_EPI_RELU,
+            "geglu": C.RAYA_EPI_GEGLU}[act]
+    out = _dev(res) if residual else torch.full((m, n), 9.0, device="cuda")
+    hip_gemm.matmul_nt_device(out, _dev(a), _dev(b), bias=_dev(bias), activation=code,
+                              residual=out if residual else None)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.abs(got - want).max() < 1e-4 * max(1.0, float(np.abs(want).max()))
