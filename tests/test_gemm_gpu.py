@@ -59,6 +59,24 @@ def test_within_the_reordering_bound(hip_gemm, m, n, k):
     assert (np.abs(got - want) <= bound(a, b)).all()
 
 
+def test_mfma_accumulation_is_full_fp32(hip_gemm):
+    """The MFMA path is no less accurate than sequential fp32: against a float64
+    product, its RMS error (relative to sum|a b|) is at most twice that of
+    Reference::matmul_nt.  A reduced-precision product (tf32, bf16 splits)
+    would be orders of magnitude worse."""
+    rng = np.random.default_rng(11)
+    m, n, k = 512, 384, 768
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k)).astype(np.float32)
+    exact = a.astype(np.float64) @ b.astype(np.float64).T
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64).T
+    e_gpu = np.abs(run(hip_gemm, a, b) - exact) / scale
+    e_seq = np.abs(oracle.matmul_nt(a, b, threads=8) - exact) / scale
+    rms_gpu, rms_seq = np.sqrt((e_gpu ** 2).mean()), np.sqrt((e_seq ** 2).mean())
+    print(f"rms relative error: mfma {rms_gpu:.3g}, sequential {rms_seq:.3g}")
+    assert rms_gpu <= 2 * rms_seq
+
+
 def _dev(x):
     return torch.from_numpy(np.ascontiguousarray(x)).cuda()
 
