@@ -148,19 +148,20 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
 
+    # One event pair on the launch stream brackets the K back-to-back launches
+    # (an event between launches costs ~10 us of idle queue per step), so the
+    # average launch duration is the bracketed time over K.
     log(f"timing {args.steps} steps")
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
+    start.record(stream)
+    for _ in range(args.steps):
         step()
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = [a.elapsed_time(e) for a, e in zip(starts, ends)]
-    avg_kernel_s = statistics.mean(kernel_ms) / 1e3
+    avg_kernel_s = start.elapsed_time(end) / 1e3 / args.steps
     ms_per_step = wall / args.steps * 1e3
 
     result = {
@@ -180,7 +181,7 @@ def main() -> int:
                    "mask": f"block_diag({block})", "valid_len": f"uniform [{lo}, {hi}]",
                    "outliers": "1% x20" if outliers else "none", "flop_per_step": flops,
                    "bytes_per_step": nbytes},
-        "kernel_ms": statistics.mean(kernel_ms),
+        "kernel_ms": avg_kernel_s * 1e3,
         "kernel_tflops": flops / avg_kernel_s / 1e12,
         "mfma_frac": flops / avg_kernel_s / 1e12 / PEAK_FP32_MFMA_TFLOPS,
     }
