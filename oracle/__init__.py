@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_erf.restype = _dbl
         L.oracle_gelu.argtypes = [_f32]
         L.oracle_gelu.restype = _f32
+        L.oracle_gelu_vec.argtypes = [_fp, _fp, _u64]
         L.oracle_layer_norm.argtypes = [_fp, _fp, _fp, _fp, _f32, _u64, _u64]
         L.oracle_softmax.argtypes = [_fp, _u64]
         L.oracle_rope.argtypes = [_fp, _u64, _u64, _u64, _f32]
@@ -160,8 +161,9 @@ def gelu(x: float) -> float:
 
 def gelu_array(x) -> np.ndarray:
     x = _c32(x)
-    f = lib().oracle_gelu
-    return np.array([f(float(t)) for t in x.ravel()], dtype=np.float32).reshape(x.shape)
+    out = np.empty_like(x)
+    lib().oracle_gelu_vec(_f(out), _f(x), x.size)
+    return out
 
 
 def layer_norm(x, weight, bias, eps):

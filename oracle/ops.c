@@ -43,6 +43,11 @@ float oracle_gelu(float x) {
     return (float)(0.5 * xd * (1.0 + oracle_erf(xd * 0.70710678118654752440)));
 }
 
+/* ops::gelu over an array. */
+void oracle_gelu_vec(float *out, const float *x, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) out[i] = oracle_gelu(x[i]);
+}
+
 /* ops::layer_norm, ops.rs:51-74: f64 mean and biased variance per row. */
 void oracle_layer_norm(float *out, const float *x, const float *weight, const float *bias,
                        float eps, uint64_t rows, uint64_t d) {

@@ -88,6 +88,7 @@ void oracle_matmul_nt_threaded(float *out, const float *a, const float *b, uint6
 /* Scalar ops of the reference forward (crates/raya-core/src/ops.rs). */
 double oracle_erf(double x);
 float oracle_gelu(float x);
+void oracle_gelu_vec(float *out, const float *x, uint64_t n);
 void oracle_layer_norm(float *out, const float *x, const float *weight, const float *bias,
                        float eps, uint64_t rows, uint64_t d);
 void oracle_softmax(float *x, uint64_t n);
