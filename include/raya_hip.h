@@ -151,6 +151,81 @@ int raya_matmul_nt_device(float *out, int64_t ldo, const float *a, int64_t lda, 
                           int64_t ldb, uint64_t m, uint64_t n, uint64_t k,
                           const raya_gemm_epilogue *ep, void *stream);
 
+/* ---- Decision model (crates/raya-core, crates/raya-weights) ------------------------------
+ *
+ * Errors of this part are raya_core::Error (crates/raya-core/src/error.rs:5-33); the
+ * message is the variant's Display text ("invalid config: `field`: reason",
+ * "invalid input: …", "invalid weights file …" with its report, …). */
+#define RAYA_ERR_CONFIG 5        /* Error::Config, Error::Io, Error::Json */
+#define RAYA_ERR_UNIMPLEMENTED 6 /* Error::Unimplemented */
+#define RAYA_ERR_INPUT 7         /* Error::Input */
+#define RAYA_ERR_KERNEL 8        /* Error::Kernel: the attention kernel rejected the call */
+#define RAYA_ERR_WEIGHTS 9       /* Error::Weights (LoadReport) */
+
+typedef struct raya_model raya_model;
+
+/* ModelConfig::from_dir (crates/raya-core/src/config/mod.rs:26-39) on
+ * checkpoint_dir, then raya_weights::load (crates/raya-weights/src/store.rs:66-151)
+ * of weights_path (NULL: checkpoint_dir/model.safetensors, as load_dir,
+ * store.rs:234-239) against the parameter set the config implies
+ * (mapping.rs:19-143).  F16/BF16 tensors are widened to fp32.  Host only: the
+ * weights go to a device on the first forward call there, once. */
+int raya_model_load(const char *checkpoint_dir, const char *weights_path, raya_model **out);
+void raya_model_free(raya_model *model);
+
+typedef struct raya_model_info {
+    uint64_t hidden_size, intermediate_size, num_hidden_layers, num_attention_heads;
+    uint64_t global_attn_every_n_layers, local_attention, vocab_size, max_position_embeddings;
+    double global_rope_theta, local_rope_theta, norm_eps;
+    uint64_t head_layers, head_heads, head_ffn, n_act;
+    uint64_t param_floats; /* fp32 parameter storage, including per-tensor alignment */
+} raya_model_info;
+
+int raya_model_get_info(const raya_model *model, raya_model_info *info);
+
+/* A batch of ForwardInput (crates/raya-core/src/model.rs:90-100), all host
+ * arrays: sequence b has ids input_ids[b][0..seq), valid length valid_len[b]
+ * (right padding), markers marker_pos[b][0..markers) with marker_mask, and
+ * qtype[b].  A sequence with fewer markers pads with mask 0 entries (they act
+ * as invalid markers, as in the reference).  local_override != 0 replaces the
+ * local layers' Sliding(local_attention / 2) mask (encoder.rs:116-120) by
+ * (local_mask_kind, local_mask_arg) — a throughput option, not the reference. */
+typedef struct raya_forward_batch {
+    uint64_t batch, seq, markers;
+    const uint32_t *input_ids;
+    const uint64_t *valid_len;
+    const uint64_t *marker_pos;
+    const uint8_t *marker_mask;
+    const uint64_t *qtype;
+    int32_t local_override;
+    int32_t local_mask_kind;
+    uint64_t local_mask_arg;
+} raya_forward_batch;
+
+/* ForwardOutput (model.rs:102-112) per sequence, host arrays (any may be NULL):
+ * logits and probabilities [batch][markers], act_logits [batch][n_act],
+ * features [batch][4], pooled [batch][hidden_size]. */
+typedef struct raya_forward_output {
+    float *logits, *probabilities, *act_logits, *features, *pooled;
+} raya_forward_output;
+
+/* Trace (crates/raya-core/src/trace.rs): called once per stage, in execution
+ * order, under the golden fixtures' names (embedding_output, encoder_layer_00,
+ * …, act_logits) with host data valid for the call.  Sequence-shaped stages
+ * are [batch][seq][hidden] with zeros on padded rows. */
+typedef void (*raya_trace_fn)(void *user, const char *name, const uint64_t *shape, uint32_t ndim,
+                              const float *data);
+
+/* Network::forward (model.rs:261-348) for every sequence of the batch in one
+ * device pass: inputs are checked as Network::check does (model.rs:221-258)
+ * before any device work; the valid tokens are packed and run through every
+ * layer on the current device (weights uploaded there on first use); the
+ * outputs are copied back and `stream` (hipStream_t, NULL = null stream) is
+ * synchronised before returning.  trace may be NULL.  Calls on one model are
+ * serialised. */
+int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_forward_output *out,
+                       raya_trace_fn trace, void *user, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -108,7 +108,11 @@ def attend(qkv, heads, hd, theta, kind, arg, valid_len):
         q = oracle.rope(q, np.float32(theta))
         k = oracle.rope(k, np.float32(theta))
     scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
-    out = oracle.naive_attend(q, k, v, kind, valid_len, scale, window=arg)
+    # the oracle takes a BlockDiag width as `block`, a Sliding half-width as `window`
+    if kind == oracle.MASK_BLOCKDIAG:
+        out = oracle.naive_attend(q, k, v, kind, valid_len, scale, block=arg)
+    else:
+        out = oracle.naive_attend(q, k, v, kind, valid_len, scale, window=arg)
     seq = qkv.shape[0]
     return np.ascontiguousarray(out.transpose(1, 0, 2).reshape(seq, heads * hd))
 

@@ -14,6 +14,7 @@ RAYA_OK, RAYA_ERR_SHAPE, RAYA_ERR_LENGTH, RAYA_ERR_UNSUPPORTED, RAYA_ERR_DEVICE 
 RAYA_MASK_BLOCK3, RAYA_MASK_WINDOW64, RAYA_MASK_FULL, RAYA_MASK_SLIDING, RAYA_MASK_BLOCKDIAG = range(5)
 RAYA_BLOCK, RAYA_WINDOW = 128, 64
 RAYA_EPI_NONE, RAYA_EPI_GELU, RAYA_EPI_RELU, RAYA_EPI_GEGLU = 0, 1, 2, 3
+RAYA_ERR_CONFIG, RAYA_ERR_UNIMPLEMENTED, RAYA_ERR_INPUT, RAYA_ERR_KERNEL, RAYA_ERR_WEIGHTS = 5, 6, 7, 8, 9
 
 
 class AttnShapeC(ctypes.Structure):
@@ -50,6 +51,32 @@ class GemmEpilogueC(ctypes.Structure):
                 ("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64)]
 
 
+class ModelInfoC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
+        "global_attn_every_n_layers", "local_attention", "vocab_size", "max_position_embeddings")] + \
+        [(n, ctypes.c_double) for n in ("global_rope_theta", "local_rope_theta", "norm_eps")] + \
+        [(n, ctypes.c_uint64) for n in ("head_layers", "head_heads", "head_ffn", "n_act",
+                                        "param_floats")]
+
+
+class ForwardBatchC(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_uint64), ("seq", ctypes.c_uint64), ("markers", ctypes.c_uint64),
+                ("input_ids", ctypes.c_void_p), ("valid_len", ctypes.c_void_p),
+                ("marker_pos", ctypes.c_void_p), ("marker_mask", ctypes.c_void_p),
+                ("qtype", ctypes.c_void_p), ("local_override", ctypes.c_int32),
+                ("local_mask_kind", ctypes.c_int32), ("local_mask_arg", ctypes.c_uint64)]
+
+
+class ForwardOutputC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("logits", "probabilities", "act_logits", "features", "pooled")]
+
+
+TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p,
+                            ctypes.POINTER(ctypes.c_uint64), ctypes.c_uint32,
+                            ctypes.POINTER(ctypes.c_float))
+
 _fp = ctypes.POINTER(ctypes.c_float)
 _vp = ctypes.c_void_p
 _sz = ctypes.c_size_t
@@ -66,6 +93,11 @@ SIGNATURES = [
     ("raya_matmul_nt", ctypes.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _u64, _u64, _u64]),
     ("raya_matmul_nt_device", ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _u64, _u64, _u64,
                                              ctypes.POINTER(GemmEpilogueC), _vp]),
+    ("raya_model_load", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    ("raya_model_free", None, [_vp]),
+    ("raya_model_get_info", ctypes.c_int, [_vp, ctypes.POINTER(ModelInfoC)]),
+    ("raya_model_forward", ctypes.c_int, [_vp, ctypes.POINTER(ForwardBatchC),
+                                          ctypes.POINTER(ForwardOutputC), TRACE_FN, _vp, _vp]),
 ]
 
 _lib = None

@@ -195,8 +195,15 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
     const float q_sign = a.scale < 0.f ? -1.f : 1.f;
 
     const Item it = decode(a, scatter(blockIdx.x, total_items, half_bits), n_qt);
-    float *ob = a.out + (int64_t)it.b * a.o_bs + (int64_t)it.h * a.o_hs;
+    // Packed sequences start at a row offset and have no padded rows in memory.
+    const bool packed = a.seq_start != nullptr;
+    const int64_t row0 = packed ? (int64_t)a.seq_start[it.b] : 0;
+    const auto base = [&](int64_t bs, int64_t hs, int64_t rs) {
+        return (packed ? row0 * rs : (int64_t)it.b * bs) + (int64_t)it.h * hs;
+    };
+    float *ob = a.out + base(a.o_bs, a.o_hs, a.o_rs);
     if (it.k_lo >= it.k_hi) {  // every row is padding: write zeros
+        if (packed) return;
         for (int c = tid; c < kQRows * CH; c += kThreads) {
             const int r = it.q0 + c / CH, c4 = c % CH;
             if (r < a.seq && c4 < dch)
@@ -217,8 +224,7 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
     // Q slice of this lane: row qi, dims [g DQ, g DQ + DQ).
     float qreg[DQ];
     {
-        const float *qp = a.q + (int64_t)it.b * a.q_bs + (int64_t)it.h * a.q_hs +
-                          (int64_t)qi * a.q_rs + g * DQ;
+        const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qi * a.q_rs + g * DQ;
 #pragma unroll
         for (int c = 0; c < DQ / 4; ++c) {
             float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -230,8 +236,8 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
         }
     }
 
-    const float *kb = a.k + (int64_t)it.b * a.k_bs + (int64_t)it.h * a.k_hs;
-    const float *vb = a.v + (int64_t)it.b * a.v_bs + (int64_t)it.h * a.v_hs;
+    const float *kb = a.k + base(a.k_bs, a.k_hs, a.k_rs);
+    const float *vb = a.v + base(a.v_bs, a.v_hs, a.v_rs);
     // Direct loads of this wave: LDS chunk slots (wave LPW + j) 64 + lane.
     auto stage = [&](int kt) {
         const int kend = min(kt + kKeys, it.k_hi);
@@ -356,7 +362,7 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
 
     // Register r of oacc[n] holds dim g DQ + NT r + n of row qi; rows at or
     // beyond valid hold zeros (every key was masked) and are stored as such.
-    if (qi < a.seq) {
+    if (qi < (packed ? valid : a.seq)) {
         const float inv = (qi < valid && l > 0.f) ? 1.f / l : 0.f;
         float *orow = ob + (int64_t)qi * a.o_rs + g * DQ;
 #pragma unroll

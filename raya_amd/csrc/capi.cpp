@@ -15,7 +15,6 @@
 #include "raya_hip.h"
 
 namespace raya {
-namespace {
 
 thread_local raya_error g_err = {RAYA_OK, {0}, 0, 0, {0}};
 
@@ -51,6 +50,8 @@ int ok() {
     g_err.message[0] = 0;
     return RAYA_OK;
 }
+
+namespace {
 
 // Mask and parameter checks shared by both attention entry points.  The first
 // four checks restate validate() (attention.rs:128-158) in its order.

@@ -1,0 +1,189 @@
+// Row-wise kernels of the device-resident decision-model forward: embedding
+// gather + LayerNorm, LayerNorm (+ per-sequence vector add), rotary embedding on
+// the packed QKV projection, marker-row gather, and the per-sequence tail of the
+// head (marker mask, softmax, score features, act-head input).
+//
+// Rows are tokens of a packed batch: sequence b owns rows
+// [seq_start[b], seq_start[b] + valid_len[b]) and padded positions are never
+// materialised.  Every kernel is HBM-bound; one wave handles one row so that
+// loads are coalesced along the hidden dimension.
+#include <cmath>
+
+#include "internal.hpp"
+
+namespace raya {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one wave per row, four waves per workgroup
+
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+    return x;
+}
+
+// ops::layer_norm (crates/raya-core/src/ops.rs:51-74): mean and biased variance
+// in f64, y = f32((x - mean) * inv) * w (+ b).  The statistics are reduced in a
+// different order than the reference's sequential sums, which moves them by a
+// few f64 ulps and the f32 result by at most one ulp in rare rounding ties.
+// When `add` is given, out_add = y + add[add_row(row)] (the type embedding of
+// the row's sequence, model.rs:297-303).
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+    layer_norm_kernel(const float *x, int64_t ldx, const int32_t *gather, const float *w,
+                      const float *b, float eps, int rows, int d, float *out, int64_t ldo,
+                      const float *add, const int32_t *row_seq, const int32_t *seq_index,
+                      float *out_add) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int64_t src = gather ? (int64_t)gather[row] : (int64_t)row;
+    const float *xr = x + src * ldx;
+    double s = 0.0;
+    for (int c = lane; c < d; c += 64) s += (double)xr[c];
+    const double mean = wave_sum(s) / (double)d;
+    double v = 0.0;
+    for (int c = lane; c < d; c += 64) {
+        const double t = (double)xr[c] - mean;
+        v += t * t;
+    }
+    const double var = wave_sum(v) / (double)d;
+    const double inv = 1.0 / sqrt(var + (double)eps);
+    const float *addr = nullptr;
+    if (add) addr = add + (int64_t)seq_index[row_seq[row]] * d;
+    for (int c = lane; c < d; c += 64) {
+        float y = __fmul_rn((float)(((double)xr[c] - mean) * inv), w[c]);
+        if (b) y = __fadd_rn(y, b[c]);
+        if (out) out[(int64_t)row * ldo + c] = y;
+        if (out_add) out_add[(int64_t)row * ldo + c] = __fadd_rn(y, addr[c]);
+    }
+}
+
+// ops::rope_in_place (ops.rs:118-141) on the q and k sections of a packed
+// [rows][3 d] projection: for head h and i < half, (a, b) = (x[i], x[i + half])
+// becomes (a cos - b sin, b cos + a sin) at the row's position.  Each product
+// and the sum are rounded separately, as the reference's scalar code does.
+__global__ void rope_kernel(float *qkv, int64_t ld, const int32_t *positions, const float *cos_t,
+                            const float *sin_t, int rows, int d, int head_dim) {
+    const int half = head_dim / 2;
+    const int per_row = d / head_dim * half * 2;  // (q, k) x heads x half
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * per_row) return;
+    const int row = (int)(idx / per_row);
+    int rem = (int)(idx % per_row);
+    const int sec = rem / (d / 2);  // 0: q, 1: k
+    rem %= d / 2;
+    const int h = rem / half, i = rem % half;
+    float *p = qkv + (int64_t)row * ld + sec * d + h * head_dim;
+    const int64_t t = (int64_t)positions[row] * half + i;
+    const float c = cos_t[t], s = sin_t[t];
+    const float a = p[i], bb = p[i + half];
+    p[i] = __fsub_rn(__fmul_rn(a, c), __fmul_rn(bb, s));
+    p[i + half] = __fadd_rn(__fmul_rn(bb, c), __fmul_rn(a, s));
+}
+
+// out[j] = h[rows[j]] (zeros where rows[j] < 0).
+__global__ void gather_rows_kernel(const float *h, int64_t ldh, const int32_t *rows, int n, int d,
+                                   float *out) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)n * d) return;
+    const int j = (int)(idx / d), c = (int)(idx % d);
+    const int r = rows[j];
+    out[idx] = r >= 0 ? h[(int64_t)r * ldh + c] : 0.0f;
+}
+
+// The tail of Network::forward (model.rs:310-334) and head::features
+// (head.rs:70-92) for one sequence per thread, in the reference's sequential
+// f32 order: invalid markers' logits become -1e4, softmax_in_place
+// (ops.rs:77-87), [top1, top1 - top2, entropy / ln k, k / 255] with
+// k = max(valid markers, 2), pooled = row 0, act_in = [pooled, features].
+__global__ void head_finish_kernel(const float *raw_logits, const uint8_t *mask, int batch,
+                                   int markers, const float *h, int64_t ldh,
+                                   const int32_t *seq_start, int d, float *logits, float *probs,
+                                   float *features, float *pooled, float *act_in) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= batch) return;
+    const float *raw = raw_logits + (int64_t)b * markers;
+    const uint8_t *mk = mask + (int64_t)b * markers;
+    float *lg = logits + (int64_t)b * markers;
+    float *pr = probs + (int64_t)b * markers;
+    float mx = -INFINITY;
+    int valid = 0;
+    for (int j = 0; j < markers; ++j) {
+        lg[j] = mk[j] ? raw[j] : -1e4f;
+        valid += mk[j] ? 1 : 0;
+        mx = fmaxf(mx, lg[j]);
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < markers; ++j) {
+        pr[j] = expf(__fsub_rn(lg[j], mx));
+        sum = __fadd_rn(sum, pr[j]);
+    }
+    for (int j = 0; j < markers; ++j) pr[j] = __fdiv_rn(pr[j], sum);
+    const float k = (float)(valid > 2 ? valid : 2);
+    float ent = 0.0f, top1 = -INFINITY, top2 = -INFINITY;
+    for (int j = 0; j < markers; ++j) {
+        const float x = pr[j];
+        ent = __fadd_rn(ent, __fmul_rn(x, logf(fmaxf(x, 1e-9f))));
+        if (x > top1) {
+            top2 = top1;
+            top1 = x;
+        } else if (x > top2) {
+            top2 = x;
+        }
+    }
+    if (markers < 2) top2 = 0.0f;
+    float f[4] = {top1, __fsub_rn(top1, top2), __fdiv_rn(-ent, logf(k)), __fdiv_rn(k, 255.0f)};
+    const float *row0 = h + (int64_t)seq_start[b] * ldh;
+    float *ai = act_in + (int64_t)b * (d + 4);
+    for (int c = 0; c < d; ++c) {
+        pooled[(int64_t)b * d + c] = row0[c];
+        ai[c] = row0[c];
+    }
+    for (int c = 0; c < 4; ++c) {
+        features[b * 4 + c] = f[c];
+        ai[d + c] = f[c];
+    }
+}
+
+unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_layer_norm(const LayerNormLaunch &l, hipStream_t stream) {
+    if (l.rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(layer_norm_kernel, dim3(blocks_for(l.rows, kRowsPerBlock)),
+                       dim3(64 * kRowsPerBlock), 0, stream, l.x, l.ldx, l.gather, l.w, l.b, l.eps,
+                       l.rows, l.d, l.out, l.ldo, l.add, l.row_seq, l.seq_index, l.out_add);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float *qkv, int64_t ld, const int32_t *positions, const float *cos_t,
+                       const float *sin_t, int rows, int d, int head_dim, hipStream_t stream) {
+    const int64_t n = (int64_t)rows * d;  // (q, k) x d / 2 pairs per row
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, qkv, ld,
+                       positions, cos_t, sin_t, rows, d, head_dim);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float *h, int64_t ldh, const int32_t *rows, int n, int d,
+                              float *out, hipStream_t stream) {
+    const int64_t total = (int64_t)n * d;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, h, ldh,
+                       rows, n, d, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_head_finish(const float *raw_logits, const uint8_t *mask, int batch, int markers,
+                              const float *h, int64_t ldh, const int32_t *seq_start, int d,
+                              float *logits, float *probs, float *features, float *pooled,
+                              float *act_in, hipStream_t stream) {
+    if (batch == 0) return hipSuccess;
+    hipLaunchKernelGGL(head_finish_kernel, dim3(blocks_for(batch, 64)), dim3(64), 0, stream,
+                       raw_logits, mask, batch, markers, h, ldh, seq_start, d, logits, probs,
+                       features, pooled, act_in);
+    return hipGetLastError();
+}
+
+}  // namespace raya

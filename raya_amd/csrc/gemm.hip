@@ -18,7 +18,10 @@
 // ReLU, encoder.rs:132-134 residual add): y = acc + bias; y = act(y);
 // out = y + residual.  For GeGLU the weight has 2n rows; a workgroup loads the
 // "input" rows j and the "gate" rows n + j side by side so that both halves of
-// an output element land in the same lane and register.
+// an output element land in the same lane and register.  The plain epilogue can
+// also apply rotary embedding (ops.rs:118-141) to the q and k sections of a
+// packed QKV projection, so encoder::attend's split_qkv + rope_in_place pass
+// (encoder.rs:36-71) is not needed.
 #include "internal.hpp"
 
 namespace raya {
@@ -62,7 +65,7 @@ __device__ __forceinline__ float4 load4(const float *base, int64_t ld, int row, 
     return x;
 }
 
-template <int ACT, bool VEC>
+template <int ACT, bool VEC, bool ROPE>
 __global__ void __launch_bounds__(kThreads) gemm_nt_kernel(const GemmLaunch g) {
     __shared__ __attribute__((aligned(16))) float As[BM * SA];
     __shared__ __attribute__((aligned(16))) float Bs[BN * SA];
@@ -170,15 +173,33 @@ __global__ void __launch_bounds__(kThreads) gemm_nt_kernel(const GemmLaunch g) {
                 if (g.residual) y += g.residual[(int64_t)row * g.ldr + col];
                 g.out[(int64_t)row * g.ldo + col] = y;
             } else {
+                float y[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn + 32 * j + li;
+                    y[j] = acc[i][j][r];
+                    if (g.bias && col < g.n) y[j] += g.bias[col];
+                    y[j] = activate<ACT>(y[j]);
+                }
+                if constexpr (ROPE) {
+                    // Columns c and c + 32 of one 64-wide head sit in the same lane
+                    // and register of acc[i][0] and acc[i][1].
+                    const int col0 = n0 + wn + li;
+                    if (col0 < g.rope_cols) {
+                        const int64_t t = (int64_t)g.positions[row] * (kRopeHeadDim / 2) + li;
+                        const float c = g.rope_cos[t], sn = g.rope_sin[t];
+                        const float x0 = y[0], x1 = y[1];
+                        y[0] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+                        y[1] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, sn));
+                    }
+                }
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int col = n0 + wn + 32 * j + li;
                     if (col >= g.n) continue;
-                    float y = acc[i][j][r];
-                    if (g.bias) y += g.bias[col];
-                    y = activate<ACT>(y);
-                    if (g.residual) y += g.residual[(int64_t)row * g.ldr + col];
-                    g.out[(int64_t)row * g.ldo + col] = y;
+                    float v = y[j];
+                    if (g.residual) v += g.residual[(int64_t)row * g.ldr + col];
+                    g.out[(int64_t)row * g.ldo + col] = v;
                 }
             }
         }
@@ -192,10 +213,24 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
     if (tiles > 0x7fffffff / kThreads) return hipErrorInvalidValue;
     const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (((uintptr_t)g.a & 15) == 0) &&
                      (((uintptr_t)g.b & 15) == 0) && (g.k % 4 == 0);
+    const dim3 grid((unsigned)tiles), block(kThreads);
+    if constexpr (ACT == RAYA_EPI_NONE) {
+        if (g.rope_cos) {
+            // The pairing (c, c + 32) needs 64-wide heads aligned to the 64-column wave tiles.
+            if (g.rope_cols % kRopeHeadDim != 0 || g.rope_cols > g.n) return hipErrorInvalidValue;
+            if (vec)
+                hipLaunchKernelGGL((gemm_nt_kernel<ACT, true, true>), grid, block, 0, stream, g);
+            else
+                hipLaunchKernelGGL((gemm_nt_kernel<ACT, false, true>), grid, block, 0, stream, g);
+            return hipGetLastError();
+        }
+    } else if (g.rope_cos) {
+        return hipErrorInvalidValue;
+    }
     if (vec)
-        hipLaunchKernelGGL((gemm_nt_kernel<ACT, true>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, g);
+        hipLaunchKernelGGL((gemm_nt_kernel<ACT, true, false>), grid, block, 0, stream, g);
     else
-        hipLaunchKernelGGL((gemm_nt_kernel<ACT, false>), dim3((unsigned)tiles), dim3(kThreads), 0, stream, g);
+        hipLaunchKernelGGL((gemm_nt_kernel<ACT, false, false>), grid, block, 0, stream, g);
     return hipGetLastError();
 }
 

@@ -23,6 +23,10 @@ struct AttnLaunch {
     int32_t mask_kind;
     int32_t mask_arg;  // Sliding half-width / BlockDiag width, clamped to seq
     float scale;
+    // Packed sequences: when set, sequence b's rows start at row seq_start[b] of
+    // each operand (batch strides unused), only its valid rows exist and rows at
+    // or beyond valid_len are neither read nor written.
+    const int32_t *seq_start;
 };
 
 // Largest head_dim the fused attention kernel is instantiated for.
@@ -44,9 +48,50 @@ struct GemmLaunch {
     const float *bias;
     const float *residual;
     int64_t ldr;
+    // Rotary embedding fused into a plain (RAYA_EPI_NONE) epilogue: columns below
+    // rope_cols (the q and k sections of a packed QKV projection, head_dim 64)
+    // are rotated in pairs (c, c + 32) at position positions[row], with
+    // cos/sin tables [position][32].  rope_cos == nullptr disables it.
+    const float *rope_cos, *rope_sin;
+    const int32_t *positions;
+    int32_t rope_cols;
 };
+
+// Head dim of the fused RoPE epilogue (other head dims use launch_rope).
+constexpr int kRopeHeadDim = 64;
 
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);
 hipError_t launch_fill_zero(float *out, int64_t ldo, int m, int n, hipStream_t stream);
+
+// Row-wise LayerNorm over `rows` rows of width d (see encoder.hip).
+struct LayerNormLaunch {
+    const float *x;
+    int64_t ldx;
+    const int32_t *gather;  // nullptr, or the source row of each output row (embedding ids)
+    const float *w, *b;     // b may be nullptr
+    float eps;
+    int32_t rows, d;
+    float *out;  // may be nullptr when out_add is set
+    int64_t ldo;
+    const float *add;          // nullptr, or a table whose row seq_index[row_seq[row]] is added
+    const int32_t *row_seq;    // sequence of each row
+    const int32_t *seq_index;  // table row of each sequence
+    float *out_add;
+};
+
+hipError_t launch_layer_norm(const LayerNormLaunch &l, hipStream_t stream);
+hipError_t launch_rope(float *qkv, int64_t ld, const int32_t *positions, const float *cos_t,
+                       const float *sin_t, int rows, int d, int head_dim, hipStream_t stream);
+hipError_t launch_gather_rows(const float *h, int64_t ldh, const int32_t *rows, int n, int d,
+                              float *out, hipStream_t stream);
+hipError_t launch_head_finish(const float *raw_logits, const uint8_t *mask, int batch, int markers,
+                              const float *h, int64_t ldh, const int32_t *seq_start, int d,
+                              float *logits, float *probs, float *features, float *pooled,
+                              float *act_in, hipStream_t stream);
+
+// Thread-local error state of the C ABI (capi.cpp).
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail_device(hipError_t e, const char *what);
+int ok();
 
 }  // namespace raya

@@ -1,0 +1,186 @@
+"""Parity of the device-resident decision-model forward with the reference, through the C ABI.
+
+* The four forward goldens (crates/raya-cli/tests/forward_golden.rs): every traced stage
+  on the valid rows at 1e-5, probabilities and features at 1e-6.  fixture-h64 has
+  head_dim 32 (separate RoPE kernel), fixture-h128 head_dim 64 (RoPE fused into the
+  QKV GEMM epilogue).
+* Padding invariance (forward_golden.rs:238-262).
+* A batch of sequences with different lengths and markers against the oracle's
+  Network::forward run one sequence at a time, on random models of both head dims.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import forward as F
+from raya_amd import Mask
+from raya_amd import model as M
+from tests.conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+FWD = os.path.join(GOLDEN, "forward")
+LAYER_TOL, PROB_TOL = 1e-5, 1e-6
+CASES = ["short", "medium", "padded", "fastpath_off"]
+
+
+def load_case(name):
+    from safetensors.numpy import load_file
+
+    meta = json.load(open(os.path.join(FWD, name, "meta.json")))
+    cdir = os.path.normpath(os.path.join(FWD, name, meta["config_dir"]))
+    wpath = os.path.normpath(os.path.join(FWD, name, meta["weights_file"]))
+    g = load_file(os.path.join(FWD, name, "tensors.safetensors"))
+    return F.load_config(cdir), M.Model.load(cdir, wpath), g, meta["input"]["unpadded_length"]
+
+
+def golden_input(g, valid, cut=None):
+    ids = g["input_ids"][0] if cut is None else g["input_ids"][0][:cut]
+    return M.ForwardInput(ids, valid, g["marker_pos"][0], g["marker_mask"][0], int(g["qtype"][0]))
+
+
+def stages(cfg):
+    v = [("embedding_output", LAYER_TOL)]
+    v += [(f"encoder_layer_{i:02d}", LAYER_TOL) for i in range(cfg.layers)]
+    v += [(n, LAYER_TOL) for n in ("encoder_final_norm", "encoder_output", "type_emb_add", "head_input")]
+    v += [(f"head_layer_{i:02d}", LAYER_TOL) for i in range(cfg.head_layers)]
+    v += [("marker_states", LAYER_TOL), ("logits", LAYER_TOL), ("probabilities", PROB_TOL),
+          ("act_features", PROB_TOL), ("pooled", LAYER_TOL), ("act_logits", LAYER_TOL)]
+    return v
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_forward_matches_golden(case):
+    cfg, model, g, valid = load_case(case)
+    print(f"case {case}: valid {valid} of {g['input_ids'].shape[1]}", flush=True)
+    tr = M.Trace()
+    out = model.forward(golden_input(g, valid), trace=tr)
+    assert tr.names() == [n for n, _ in stages(cfg)]
+    seq = g["input_ids"].shape[1]
+    worst = {}
+    for name, tol in stages(cfg):
+        want = g[name].astype(np.float32)
+        shape, got = tr.get(name)
+        assert shape == want.shape, name
+        if want.ndim == 3 and want.shape[1] == seq:
+            want, got = want[:, :valid], got[:, :valid]
+        worst[name] = float(np.abs(got - want).max())
+        assert worst[name] <= tol, (name, worst[name])
+    print(case, {k: f"{v:.1e}" for k, v in worst.items()})
+    for name, arr in (("logits", out.logits), ("probabilities", out.probabilities),
+                      ("act_logits", out.act_logits), ("pooled", out.pooled)):
+        assert np.array_equal(arr, tr.get(name)[1].reshape(arr.shape)), name
+    assert np.array_equal(out.features, tr.get("act_features")[1].reshape(4))
+
+
+def test_padding_does_not_change_valid_rows():
+    cfg, model, g, valid = load_case("padded")
+    a, b = M.Trace(), M.Trace()
+    model.forward(golden_input(g, valid), trace=a)
+    model.forward(golden_input(g, valid, cut=valid), trace=b)
+    for name in ("embedding_output", "encoder_layer_00", "encoder_layer_02", "head_layer_00"):
+        x, y = a.get(name)[1][:, :valid], b.get(name)[1][:, :valid]
+        assert np.abs(x - y).max() <= 1e-5, name
+    for name in ("logits", "probabilities", "act_logits", "pooled"):
+        assert np.abs(a.get(name)[1] - b.get(name)[1]).max() <= 1e-5, name
+
+
+# --- random models against the oracle -------------------------------------------------------
+
+def make_model(tmp_path, hidden, heads, layers=3, inter=None, head_layers=2, vocab=300, acts=2,
+               local_attention=16, seed=0, dtype=np.float32):
+    from safetensors.numpy import save_file
+
+    inter = inter or 2 * hidden
+    enc = {"hidden_size": hidden, "intermediate_size": inter, "num_hidden_layers": layers,
+           "num_attention_heads": heads, "global_attn_every_n_layers": 2,
+           "local_attention": local_attention, "max_position_embeddings": 4096,
+           "vocab_size": vocab, "norm_eps": 1e-5, "norm_bias": False, "attention_bias": False,
+           "mlp_bias": False, "hidden_activation": "gelu",
+           "rope_parameters": {"full_attention": {"rope_theta": 160000.0},
+                               "sliding_attention": {"rope_theta": 10000.0}}}
+    agent = {"head_layers": head_layers, "act_costs": {f"a{i}": 0.1 for i in range(acts - 1)}}
+    d = tmp_path / f"m{hidden}_{heads}_{seed}"
+    os.makedirs(d / "encoder", exist_ok=True)
+    json.dump(enc, open(d / "encoder" / "config.json", "w"))
+    json.dump(agent, open(d / "rl_agent_config.json", "w"))
+    cfg = F.load_config(str(d))
+    rng = np.random.default_rng(seed)
+    w = {}
+    for name, shape in F.expected_names(cfg):
+        if name.endswith("norm.weight") or name.endswith(("norm1.weight", "norm2.weight")) \
+                or name == "scorer.0.weight":
+            x = 1.0 + 0.1 * rng.standard_normal(shape)
+        else:
+            x = 0.05 * rng.standard_normal(shape)
+        w[name] = x.astype(dtype)
+    save_file(w, str(d / "model.safetensors"))
+    return cfg, str(d), {k: v.astype(np.float32) for k, v in w.items()}
+
+
+def random_batch(rng, cfg, b, seq, k):
+    ids = rng.integers(1, cfg.vocab, size=(b, seq)).astype(np.uint32)
+    valid = rng.integers(max(4, seq // 4), seq + 1, size=b)
+    valid[0] = seq
+    pos = np.zeros((b, k), np.int64)
+    mask = np.zeros((b, k), bool)
+    for i in range(b):
+        nk = rng.integers(1, k + 1)
+        pos[i, :nk] = np.sort(rng.choice(valid[i], size=nk, replace=False))
+        mask[i, :nk] = True
+        mask[i, 0] = True
+    qtype = rng.integers(0, 3, size=b)
+    return ids, valid, pos, mask, qtype
+
+
+@pytest.mark.parametrize("hidden,heads", [(128, 2), (64, 2)])
+def test_batch_matches_oracle_per_sequence(tmp_path, hidden, heads):
+    cfg, cdir, w = make_model(tmp_path, hidden, heads)
+    model = M.Model.load(cdir)
+    rng = np.random.default_rng(hidden)
+    ids, valid, pos, mask, qtype = random_batch(rng, cfg, b=5, seq=200, k=4)
+    print(f"hidden {hidden} heads {heads}: valid {valid.tolist()}", flush=True)
+    out = model.forward_batch(ids, valid, pos, mask, qtype)
+    for i in range(len(valid)):
+        want = F.forward(cfg, w, ids[i], int(valid[i]), pos[i], mask[i], int(qtype[i]))
+        for name, tol in (("logits", LAYER_TOL), ("probabilities", PROB_TOL),
+                          ("act_logits", LAYER_TOL), ("features", PROB_TOL), ("pooled", LAYER_TOL)):
+            got, exp = getattr(out, name)[i], getattr(want, name)
+            assert np.abs(got - exp).max() <= tol, (i, name, float(np.abs(got - exp).max()))
+        # the same sequence alone on the device gives the same outputs
+        one = model.forward(M.ForwardInput(ids[i], int(valid[i]), pos[i], mask[i], int(qtype[i])))
+        assert np.abs(one.act_logits - out.act_logits[i]).max() <= 1e-6
+
+
+def test_local_mask_override_matches_oracle(tmp_path):
+    """The throughput option: BlockDiag(64) on local layers, global layers stay Full."""
+    cfg, cdir, w = make_model(tmp_path, 128, 2, layers=2, head_layers=0)
+    model = M.Model.load(cdir)
+    rng = np.random.default_rng(3)
+    ids, valid, pos, mask, qtype = random_batch(rng, cfg, b=3, seq=300, k=3)
+    tr = M.Trace()
+    out = model.forward_batch(ids, valid, pos, mask, qtype, trace=tr, local_mask=Mask.block_diag(64))
+    for i in range(3):
+        want = F.forward(cfg, w, ids[i], int(valid[i]), pos[i], mask[i], int(qtype[i]),
+                         local_mask=(oracle.MASK_BLOCKDIAG, 64))
+        v = int(valid[i])
+        got = tr.get("encoder_layer_01")[1][i, :v]
+        assert np.abs(got - want.trace["encoder_layer_01"][:v]).max() <= LAYER_TOL
+        assert np.abs(out.act_logits[i] - want.act_logits).max() <= LAYER_TOL
+
+
+def test_half_precision_weights_are_widened_exactly(tmp_path):
+    """F16 weights give the same outputs as the F32 file holding their widened values."""
+    from safetensors.numpy import save_file
+
+    cfg, cdir16, w = make_model(tmp_path, 128, 2, layers=2, seed=7, dtype=np.float16)
+    cfg, cdir32, _ = make_model(tmp_path / "f32", 128, 2, layers=2, seed=7, dtype=np.float16)
+    save_file(w, os.path.join(cdir32, "model.safetensors"))  # widened on the host by numpy
+    rng = np.random.default_rng(4)
+    batch = random_batch(rng, cfg, b=2, seq=64, k=2)
+    a = M.Model.load(cdir16).forward_batch(*batch)
+    b = M.Model.load(cdir32).forward_batch(*batch)
+    assert np.array_equal(a.act_logits, b.act_logits) and np.array_equal(a.pooled, b.pooled)
