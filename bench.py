@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of raya's block-local attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload NAME]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload NAME] [--no-encoder]
 
 A step is one launch of the fused fp32 attention kernel over one whole batch
 whose Q, K, V (seeded N(0, 1)) are already resident in HBM.  The default
@@ -10,6 +10,11 @@ mask and per-sequence valid lengths uniform in [512, 2048].  Prints one JSON
 line: TFLOP/s on the algorithmic FLOP count (valid rows only), the kernel's
 HBM roofline fraction (HIP events on the launch stream), and the reference's
 Tiled CPU algorithm timed on this host on the same inputs.
+
+With the default workload the line also carries "encoder": sequences/sec of the
+full 12-layer ModernBERT-base decision-model forward (B=64, L=512, valid
+lengths uniform in [128, 512], random N(0, 0.02) weights from a safetensors
+checkpoint) and the oracle's CPU forward on the first sequences beside it.
 """
 from __future__ import annotations
 
@@ -108,6 +113,125 @@ def cpu_baseline(qkv, valid, wl, budget_s: float):
     }
 
 
+ENCODER = {
+    # 12-layer ModernBERT-base decision model, batch of 64 sequences of up to 512 tokens
+    "workload": "encoder_b64_l512_12x768_geglu",
+    "config": 4, "batch": 64, "seq": 512, "valid": (128, 512), "cls_id": 101,
+    "ids": (1000, 30522), "markers": [1, 2], "qtype": 0,
+}
+
+
+def encoder_flops(valid, d=768, inter=3072, heads=12, layers=12, global_every=3, window=64):
+    """GEMM FLOP on valid tokens (2 d (3d + d + 2F + F) per token and layer, GeGLU Wi is
+    [2F, d]) plus attention FLOP (4 D H per allowed (query, key) pair; Full on global layers,
+    Sliding(window) on local layers)."""
+    hd = d // heads
+    gemm = sum(int(v) for v in valid) * 2 * d * (3 * d + d + 2 * inter + inter) * layers
+    attn = 0
+    for i in range(layers):
+        for v in valid:
+            v = int(v)
+            if i % global_every == 0:
+                pairs = v * v
+            else:  # sum over i of |[i - w, i + w] ∩ [0, v)|
+                pairs = sum(min(v, t + window + 1) - max(0, t - window) for t in range(v))
+            attn += 4 * hd * heads * pairs
+    return gemm, attn
+
+
+def encoder_inputs(spec):
+    import numpy as np
+
+    from raya_amd import synth
+
+    c, b, s = spec["config"], spec["batch"], spec["seq"]
+    lo, hi = spec["valid"]
+    valid = synth.integers(synth.workload_seed(c, 3), b, lo, hi).astype(np.uint64)
+    a, z = spec["ids"]
+    ids = synth.integers(synth.workload_seed(c, 6), b * s, a, z - 1).astype(np.uint32).reshape(b, s)
+    ids[:, 0] = spec["cls_id"]
+    k = len(spec["markers"])
+    pos = np.tile(np.array(spec["markers"], np.uint64), (b, 1))
+    mask = np.ones((b, k), np.uint8)
+    qtype = np.full(b, spec["qtype"], np.uint64)
+    return ids, valid, pos, mask, qtype
+
+
+def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dict:
+    """Sequences/sec of the full forward (embed, 12 layers, final norm, scorer, act head) on a
+    batch of 64; each step includes the input upload, every kernel, the output download and
+    the stream synchronisation."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from raya_amd import checkpoint, model as M
+
+    spec = ENCODER
+    tmp = tempfile.mkdtemp(prefix="raya_ckpt_")
+    try:
+        log("encoder: writing the synthetic checkpoint")
+        checkpoint.write_synthetic(tmp, seed=1000 * spec["config"] + 5)
+        m = M.Model.load(tmp)
+        ids, valid, pos, mask, qtype = encoder_inputs(spec)
+        log(f"encoder: warmup {warmup}")
+        for _ in range(warmup):
+            out = m.forward_batch(ids, valid, pos, mask, qtype)
+        log(f"encoder: timing {steps} forwards")
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = m.forward_batch(ids, valid, pos, mask, qtype)
+        dt = (time.perf_counter() - t0) / steps
+        gemm, attn = encoder_flops(valid)
+        b = spec["batch"]
+        res = {
+            "workload": spec["workload"], "batch": b, "seq": spec["seq"],
+            "valid_len": f"uniform [{spec['valid'][0]}, {spec['valid'][1]}]",
+            "valid_tokens": int(valid.sum()), "sequences_per_s": b / dt, "ms_per_forward": dt * 1e3,
+            "flop_per_forward_valid": gemm + attn, "tflops": (gemm + attn) / dt / 1e12,
+            "mfma_frac": (gemm + attn) / dt / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+            "padding": "not computed (valid tokens are packed; padded rows cannot change valid rows)",
+            "masks": "reference: Full on global layers, Sliding(64) on local layers",
+            "weights": "N(0, 0.02), norms 1, safetensors under raya-weights names, loaded once",
+            "steps": steps, "warmup": warmup,
+            "act_logits_finite": bool(np.isfinite(out.act_logits).all()),
+        }
+        if cpu:
+            log("encoder: cpu baseline")
+            res["cpu_baseline"] = encoder_cpu_baseline(tmp, ids, valid, pos, mask, qtype, out,
+                                                       cpu_seconds)
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return res
+
+
+def encoder_cpu_baseline(ckpt, ids, valid, pos, mask, qtype, gpu_out, budget_s: float) -> dict:
+    """The oracle's restatement of Network::forward (sequential-f32 GEMMs on host threads,
+    Naive attention) on the first sequences of the batch until the time budget is spent."""
+    import numpy as np
+
+    from oracle import forward as F
+
+    cfg = F.load_config(ckpt)
+    w = F.load_weights(os.path.join(ckpt, "model.safetensors"))
+    threads = min(16, len(os.sched_getaffinity(0)))
+    F.GEMM_THREADS = threads
+    done, diff, t0 = 0, 0.0, time.perf_counter()
+    while done < len(valid):
+        v = int(valid[done])
+        o = F.forward(cfg, w, ids[done, :v], v, pos[done], mask[done], int(qtype[done]))
+        diff = max(diff, float(np.abs(o.act_logits - gpu_out.act_logits[done]).max()))
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": done / dt, "unit": "sequences/s", "cores": threads, "kind": "port",
+            "sample": (f"first {done} sequences of the batch ({int(valid[:done].sum())} tokens), "
+                       f"one at a time, {dt:.1f} s"),
+            "gpu_vs_cpu_act_logits_max_abs": diff}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +240,9 @@ def main() -> int:
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true", help="skip the encoder forward leg")
+    ap.add_argument("--encoder-steps", type=int, default=10)
+    ap.add_argument("--encoder-warmup", type=int, default=2)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
@@ -202,6 +329,9 @@ def main() -> int:
             diff = max(diff, float(np.abs(got[i, :, : valid[i]] - cpu_out[i, :, : valid[i]]).max()))
         cb["gpu_vs_cpu_max_abs"] = diff
         result["cpu_baseline"] = cb
+    if args.workload == DEFAULT and not args.no_encoder:
+        result["encoder"] = bench_encoder(args.encoder_steps, args.encoder_warmup, args.cpu_seconds,
+                                          cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
 

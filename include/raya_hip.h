@@ -173,6 +173,19 @@ typedef struct raya_model raya_model;
 int raya_model_load(const char *checkpoint_dir, const char *weights_path, raya_model **out);
 void raya_model_free(raya_model *model);
 
+/* mapping::expected (crates/raya-weights/src/mapping.rs:19-40): the parameters,
+ * in order, that a weights file for the config in checkpoint_dir must hold,
+ * under raya-weights' names.  Writes min(capacity, count) entries; *count is
+ * the full number. */
+typedef struct raya_param_entry {
+    char name[128];
+    uint32_t ndim;
+    uint64_t shape[4];
+} raya_param_entry;
+
+int raya_expected_params(const char *checkpoint_dir, raya_param_entry *out, uint64_t capacity,
+                         uint64_t *count);
+
 typedef struct raya_model_info {
     uint64_t hidden_size, intermediate_size, num_hidden_layers, num_attention_heads;
     uint64_t global_attn_every_n_layers, local_attention, vocab_size, max_position_embeddings;

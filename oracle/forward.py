@@ -23,6 +23,7 @@ import numpy as np
 import oracle
 
 HEAD_EPS = np.float32(1e-5)  # head.rs:8, torch's default layer_norm_eps
+GEMM_THREADS = 4  # host threads of the sequential-f32 GEMM (results do not depend on it)
 
 
 # --- configuration (crates/raya-core/src/config/{encoder,agent,mod}.rs) -----------------------
@@ -88,7 +89,7 @@ def load_weights(path: str) -> dict[str, np.ndarray]:
 
 def linear(x, w, b=None):
     """ops::linear (ops.rs:91-109): sequential-f32 matmul_nt, then the bias in f32."""
-    out = oracle.matmul_nt(x, w, threads=4)
+    out = oracle.matmul_nt(x, w, threads=GEMM_THREADS)
     if b is not None:
         out += b
     return out

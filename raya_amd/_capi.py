@@ -51,6 +51,11 @@ class GemmEpilogueC(ctypes.Structure):
                 ("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64)]
 
 
+class ParamEntryC(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("ndim", ctypes.c_uint32),
+                ("shape", ctypes.c_uint64 * 4)]
+
+
 class ModelInfoC(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in (
         "hidden_size", "intermediate_size", "num_hidden_layers", "num_attention_heads",
@@ -95,6 +100,8 @@ SIGNATURES = [
                                              ctypes.POINTER(GemmEpilogueC), _vp]),
     ("raya_model_load", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     ("raya_model_free", None, [_vp]),
+    ("raya_expected_params", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ParamEntryC), _u64,
+                                            ctypes.POINTER(_u64)]),
     ("raya_model_get_info", ctypes.c_int, [_vp, ctypes.POINTER(ModelInfoC)]),
     ("raya_model_forward", ctypes.c_int, [_vp, ctypes.POINTER(ForwardBatchC),
                                           ctypes.POINTER(ForwardOutputC), TRACE_FN, _vp, _vp]),

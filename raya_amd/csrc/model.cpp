@@ -16,12 +16,10 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
-#include <fstream>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <set>
-#include <sstream>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -57,12 +55,22 @@ std::string shape_str(const std::vector<uint64_t> &s) {
 }
 
 int read_file(const std::string &path, std::string &out) {
-    std::ifstream f(path, std::ios::binary);
-    if (!f) return fail_io(path, errno ? errno : ENOENT);
-    std::ostringstream ss;
-    ss << f.rdbuf();
-    out = ss.str();
-    return RAYA_OK;
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f) return fail_io(path, errno);
+    int rc = RAYA_OK;
+    if (fseek(f, 0, SEEK_END) != 0) {
+        rc = fail_io(path, errno);
+    } else {
+        const long size = ftell(f);
+        if (size < 0 || fseek(f, 0, SEEK_SET) != 0) {
+            rc = fail_io(path, errno);
+        } else {
+            out.resize((size_t)size);
+            if (size > 0 && fread(&out[0], 1, (size_t)size, f) != (size_t)size) rc = fail_io(path, EIO);
+        }
+    }
+    fclose(f);
+    return rc;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -666,6 +674,26 @@ int raya_model_load(const char *checkpoint_dir, const char *weights_path, raya_m
 }
 
 void raya_model_free(raya_model *model) { delete (Model *)model; }
+
+int raya_expected_params(const char *checkpoint_dir, raya_param_entry *out, uint64_t capacity,
+                         uint64_t *count) {
+    if (!checkpoint_dir || !count) return fail(RAYA_ERR_CONFIG, "invalid config: `<root>`: no checkpoint directory");
+    Config c;
+    int rc = load_config(checkpoint_dir, c);
+    if (rc) return rc;
+    const std::pair<bool, const char *> flags[] = {
+        {c.attention_bias, "attention_bias"}, {c.mlp_bias, "mlp_bias"}, {c.norm_bias, "norm_bias"}};
+    for (const auto &f : flags)
+        if (f.first) return fail_unimplemented(std::string(f.second) + "=true (bias tensors are not part of Raya-L)");
+    const std::vector<Entry> e = expected(c);
+    *count = e.size();
+    for (uint64_t i = 0; i < e.size() && i < capacity && out; ++i) {
+        snprintf(out[i].name, sizeof out[i].name, "%s", e[i].name.c_str());
+        out[i].ndim = (uint32_t)e[i].shape.size();
+        for (size_t j = 0; j < 4; ++j) out[i].shape[j] = j < e[i].shape.size() ? e[i].shape[j] : 0;
+    }
+    return ok();
+}
 
 int raya_model_get_info(const raya_model *model, raya_model_info *info) {
     if (!model || !info) return fail(RAYA_ERR_INPUT, "invalid input: null model or info");

@@ -230,3 +230,27 @@ def test_invalid_marker_may_sit_on_padding():
         raise AssertionError(str(e))
     except Exception:
         pass
+
+
+def test_expected_params_follow_the_mapping():
+    """raya_expected_params lists mapping.rs's names and shapes in order, the same set the
+    fixture weights hold (and the oracle's restatement of the mapping)."""
+    from oracle import forward as F
+    from raya_amd import checkpoint
+
+    for cfg_dir in ("fixture-h64", "fixture-h128"):
+        got = checkpoint.expected_params(os.path.join(FWD, cfg_dir))
+        want = F.expected_names(F.load_config(os.path.join(FWD, cfg_dir)))
+        assert got == [(n, tuple(s)) for n, s in want]
+
+
+def test_synthetic_checkpoint_round_trips(tmp_path):
+    """A written checkpoint loads, with the shapes the config implies."""
+    from raya_amd import checkpoint
+
+    enc = dict(checkpoint.MODERNBERT_BASE, hidden_size=128, num_attention_heads=2,
+               intermediate_size=256, num_hidden_layers=2, vocab_size=500)
+    checkpoint.write_synthetic(str(tmp_path), encoder=enc, seed=1)
+    info = M.Model.load(str(tmp_path)).info
+    assert (info["hidden_size"], info["num_hidden_layers"], info["n_act"]) == (128, 2, 2)
+    assert info["norm_eps"] == 1e-12 and info["head_layers"] == 0
