@@ -45,10 +45,34 @@ struct Range {
     int lo, hi;
 };
 
+// Exact division of n in [0, 2^31) by a divisor d fixed per launch:
+// floor(n / d) = (n * m) >> s with s = 31 + ceil(log2 d), m = ceil(2^s / d),
+// which fits 32 bits (the error n (m d - 2^s) / (d 2^s) stays below 1 / d).
+struct FastDiv {
+    uint32_t m, s;
+};
+
+FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint32_t s = 31 + l;
+    return {(uint32_t)(((1ull << s) + d - 1) / d), s};
+}
+
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+    return (int)(((uint64_t)(uint32_t)n * f.m) >> f.s);
+}
+
+// Per-launch constants of the item decomposition.
+struct Plan {
+    int total, half_bits, n_qt;
+    FastDiv by_qt, by_heads, by_arg;  // by_arg: the BlockDiag width (1 otherwise)
+};
+
 // Mask::key_range (attention.rs:48-59) plus BlockDiag, clipped to valid.
 // mask_arg was clamped to seq by the host, so no sum below overflows int32
 // for seq < 2^30.
-__device__ __forceinline__ Range key_range(int kind, int arg, int i, int valid) {
+__device__ __forceinline__ Range key_range(int kind, int arg, FastDiv by_arg, int i, int valid) {
     int lo, hi;
     switch (kind) {
     case RAYA_MASK_BLOCK3: {
@@ -70,7 +94,7 @@ __device__ __forceinline__ Range key_range(int kind, int arg, int i, int valid) 
         hi = i + arg + 1;
         break;
     default: {  // RAYA_MASK_BLOCKDIAG
-        const int b = i / arg;
+        const int b = fdiv(i, by_arg);
         lo = b * arg;
         hi = lo + arg;
         break;
@@ -89,33 +113,29 @@ struct Item {
     int b, h, q0, valid, k_lo, k_hi;
 };
 
+// b is uniform, so the valid length comes through the scalar cache.
 __device__ __forceinline__ int clamp_valid(const AttnLaunch &a, int b) {
-    const int valid = a.valid_len ? a.valid_len[b] : a.valid_scalar;
+    const int valid = a.valid_len ? a.valid_len[__builtin_amdgcn_readfirstlane(b)] : a.valid_scalar;
     return min(max(valid, 0), a.seq);
 }
 
-__device__ __forceinline__ Item make_item(const AttnLaunch &a, int b, int h, int tile, int valid) {
+// Item `item` of the (sequence, head, tile) order.
+__device__ __forceinline__ Item decode(const AttnLaunch &a, const Plan &p, int item) {
     Item it;
-    it.b = b;
-    it.h = h;
+    const int bh = fdiv(item, p.by_qt);
+    const int tile = item - bh * p.n_qt;
+    it.b = fdiv(bh, p.by_heads);
+    it.h = bh - it.b * a.heads;
     it.q0 = tile * kQRows;
-    it.valid = valid;
-    if (it.q0 < valid) {
-        const int qlast = min(it.q0 + kQRows, valid) - 1;
-        it.k_lo = key_range(a.mask_kind, a.mask_arg, it.q0, valid).lo;
-        it.k_hi = key_range(a.mask_kind, a.mask_arg, qlast, valid).hi;
+    it.valid = clamp_valid(a, it.b);
+    if (it.q0 < it.valid) {
+        const int qlast = min(it.q0 + kQRows, it.valid) - 1;
+        it.k_lo = key_range(a.mask_kind, a.mask_arg, p.by_arg, it.q0, it.valid).lo;
+        it.k_hi = key_range(a.mask_kind, a.mask_arg, p.by_arg, qlast, it.valid).hi;
     } else {
         it.k_lo = it.k_hi = 0;
     }
     return it;
-}
-
-// Item `item` of the (sequence, head, tile) order.
-__device__ __forceinline__ Item decode(const AttnLaunch &a, int item, int n_qt) {
-    const int tile = item % n_qt;
-    const int bh = item / n_qt;
-    const int b = bh / a.heads;
-    return make_item(a, b, bh % a.heads, tile, clamp_valid(a, b));
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -153,6 +173,13 @@ constexpr int kMinWaves = DP <= 64 ? 4 : DP == 128 ? 2 : 1;
 
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
+// Workgroup barrier without the memory fence of __syncthreads: the fence would
+// wait for every outstanding LDS DMA (they count as LDS writes), including the
+// V tile that is meant to stay in flight during QK^T.  Callers order memory
+// themselves with explicit s_waitcnt; the clobber keeps the compiler from
+// moving memory operations across.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
 // Chunk (16 bytes) c of K/V row r sits at chunk swz(c, r) of the row in LDS:
 // an XOR swizzle within aligned groups of P chunks (P the largest power of two
 // dividing the chunks per row, 16 at head_dim 64).  The 16 rows an S^T
@@ -170,17 +197,18 @@ __device__ __forceinline__ int swz(int c, int r) {
 // the load latency.  Rows or dims outside the tile's valid range load a
 // clamped in-range address: their scores are masked, their V rows get weight
 // zero, and Q is zero on the padded dims.
+//
+// The body takes the K and V tiles as restrict pointers: inlined, that gives
+// their accesses distinct alias scopes, so the compiler knows the V tile's DMA
+// (still in flight during QK^T) does not write the K tile it reads.
 template <int DP>  // head_dim padded to a multiple of 16
-__global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
-    attend_kernel(const AttnLaunch a, int total_items, int half_bits) {
+__device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
+                                            float *__restrict__ vs) {
     constexpr int DQ = DP / 4;   // head-dim slice owned by one lane group
     constexpr int NT = DP / 16;  // 16-dim output tiles
     constexpr int CH = DP / 4;   // 16-byte chunks per row
     constexpr int LPW = CH / kWaves;  // direct loads per wave per tile (each 64 chunks)
-    __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
-    __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
 
-    const int n_qt = (a.seq + kQRows - 1) / kQRows;
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -194,7 +222,7 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
     const float c_exp = fabsf(a.scale) * kLog2e;
     const float q_sign = a.scale < 0.f ? -1.f : 1.f;
 
-    const Item it = decode(a, scatter(blockIdx.x, total_items, half_bits), n_qt);
+    const Item it = decode(a, p, scatter(blockIdx.x, p.total, p.half_bits));
     // Packed sequences start at a row offset and have no padded rows in memory.
     const bool packed = a.seq_start != nullptr;
     const int64_t row0 = packed ? (int64_t)a.seq_start[it.b] : 0;
@@ -215,31 +243,16 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
     const int qw = it.q0 + wave * 16;
     const int qi = qw + li;
     const int valid = it.valid;
-    const Range rr = qi < valid ? key_range(kind, arg, qi, valid) : Range{0, 0};
+    const Range rr = qi < valid ? key_range(kind, arg, p.by_arg, qi, valid) : Range{0, 0};
     const bool wave_live = qw < valid;
     const bool wave_full_rows = qw + 15 < valid;
-    const Range w_first = key_range(kind, arg, min(qw, valid - 1), valid);
-    const Range w_last = key_range(kind, arg, min(qw + 15, valid - 1), valid);
-
-    // Q slice of this lane: row qi, dims [g DQ, g DQ + DQ).
-    float qreg[DQ];
-    {
-        const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qi * a.q_rs + g * DQ;
-#pragma unroll
-        for (int c = 0; c < DQ / 4; ++c) {
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (qi < valid && g * DQ + 4 * c < D) x = *(const float4 *)(qp + 4 * c);
-            qreg[4 * c + 0] = x.x * q_sign;
-            qreg[4 * c + 1] = x.y * q_sign;
-            qreg[4 * c + 2] = x.z * q_sign;
-            qreg[4 * c + 3] = x.w * q_sign;
-        }
-    }
+    const Range w_first = key_range(kind, arg, p.by_arg, min(qw, valid - 1), valid);
+    const Range w_last = key_range(kind, arg, p.by_arg, min(qw + 15, valid - 1), valid);
 
     const float *kb = a.k + base(a.k_bs, a.k_hs, a.k_rs);
     const float *vb = a.v + base(a.v_bs, a.v_hs, a.v_rs);
     // Direct loads of this wave: LDS chunk slots (wave LPW + j) 64 + lane.
-    auto stage = [&](int kt) {
+    auto stage = [&](const float *src, int64_t rs, float *lds, int kt) {
         const int kend = min(kt + kKeys, it.k_hi);
 #pragma unroll
         for (int j = 0; j < LPW; ++j) {
@@ -248,12 +261,33 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
             const int c = min(swz<CH>(p, r), dch - 1);
             const int64_t row = min(kt + r, kend - 1);
             const int lds_off = (wave * LPW + j) * 64 * 16;
-            __builtin_amdgcn_global_load_lds(kb + row * a.k_rs + 4 * c,
-                                             (lds_ptr_t *)((char *)ks + lds_off), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vb + row * a.v_rs + 4 * c,
-                                             (lds_ptr_t *)((char *)vs + lds_off), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src + row * rs + 4 * c, (lds_ptr_t *)((char *)lds + lds_off),
+                                             16, 0, 0);
         }
     };
+    // Loads return in issue order, so vmcnt(LPW) means everything but the LPW V
+    // loads this wave issued last has landed.
+    constexpr int kWaitAllButV = 0xF70 | (LPW & 0xF) | ((LPW >> 4) << 14);
+
+    // K of the first tile goes out first, then Q (loaded unconditionally from a
+    // clamped in-range address so all its loads are in flight together; the
+    // out-of-range parts are zeroed after the wait), then V, which is only
+    // waited for after QK^T and the softmax.
+    stage(kb, a.k_rs, ks, it.k_lo);
+    float qreg[DQ];
+    {
+        const int qrow = min(qi, valid - 1);
+        const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qrow * a.q_rs;
+#pragma unroll
+        for (int c = 0; c < DQ / 4; ++c) {
+            const float4 x = *(const float4 *)(qp + min(g * DQ + 4 * c, D - 4));
+            qreg[4 * c + 0] = x.x;
+            qreg[4 * c + 1] = x.y;
+            qreg[4 * c + 2] = x.z;
+            qreg[4 * c + 3] = x.w;
+        }
+    }
+    stage(vb, a.v_rs, vs, it.k_lo);
 
     floatx4 oacc[NT];
 #pragma unroll
@@ -266,30 +300,40 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
     const int k_row0 = 4 * (li & 3) + (li >> 2);
 
     for (int kt = it.k_lo; kt < it.k_hi; kt += kKeys) {
-        if (kt != it.k_lo) __syncthreads();  // the previous tile's LDS reads are done
-        stage(kt);
-        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's loads have landed
-        __syncthreads();
-
-        if (!wave_live || kt >= w_last.hi || kt + kKeys <= w_first.lo) continue;
-
+        if (kt != it.k_lo) {
+            // The previous tile's LDS reads have returned (the MFMAs consumed them).
+            barrier_only();
+            stage(kb, a.k_rs, ks, kt);
+            stage(vb, a.v_rs, vs, kt);
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitAllButV);  // this wave's K (and Q) loads have landed
+        barrier_only();                            // ... and every other wave's
+        if (kt == it.k_lo) {
+            // Q is zero on rows at or beyond valid and on dims at or beyond D; a
+            // negative scale is carried by negating Q.
+#pragma unroll
+            for (int c = 0; c < DQ / 4; ++c) {
+                const bool in = qi < valid && g * DQ + 4 * c < D;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qreg[4 * c + e] = in ? qreg[4 * c + e] * q_sign : 0.f;
+            }
+        }
+        const bool active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
         floatx4 sacc[4];
+        if (active) {
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             sacc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
             const int row = 16 * t + k_row0;
             const float *kp = ks + row * DP;
-            float kop[DQ];
 #pragma unroll
             for (int c = 0; c < DQ / 4; ++c) {
                 const float4 x = *(const float4 *)(kp + 4 * swz<CH>(g * (DQ / 4) + c, row));
-                kop[4 * c + 0] = x.x;
-                kop[4 * c + 1] = x.y;
-                kop[4 * c + 2] = x.z;
-                kop[4 * c + 3] = x.w;
+                sacc[t] = mfma(x.x, qreg[4 * c + 0], sacc[t]);
+                sacc[t] = mfma(x.y, qreg[4 * c + 1], sacc[t]);
+                sacc[t] = mfma(x.z, qreg[4 * c + 2], sacc[t]);
+                sacc[t] = mfma(x.w, qreg[4 * c + 3], sacc[t]);
             }
-#pragma unroll
-            for (int kk = 0; kk < DQ; ++kk) sacc[t] = mfma(kop[kk], qreg[kk], sacc[t]);
         }
 
         // Register (t, r) of lane (g, li) is the raw score of key
@@ -329,6 +373,11 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
                 sacc[t][r] = fast_exp2((sacc[t][r] - m_use) * c_exp);
                 l += sacc[t][r];
             }
+
+        }
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's V loads have landed
+        barrier_only();
+        if (!active) continue;
 
         // O^T tile n: A-row i is dim NT i + n, so one lane reads NT contiguous
         // floats of a V row for all n at once.
@@ -379,6 +428,13 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>)
     }
 }
 
+template <int DP>
+__global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_kernel(const AttnLaunch a, const Plan p) {
+    __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
+    __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
+    attend_body<DP>(a, p, ks, vs);
+}
+
 // Half the bit width of the scatter domain: the smallest h with 4^h >= total.
 int scatter_half_bits(int64_t total) {
     int h = 1;
@@ -391,8 +447,14 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const int64_t n_qt = (a.seq + kQRows - 1) / kQRows;
     const int64_t total = n_qt * a.heads * a.batch;
     if (total > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attend_kernel<DP>, dim3((unsigned)total), dim3(kThreads), 0, stream, a,
-                       (int)total, scatter_half_bits(total));
+    Plan p;
+    p.total = (int)total;
+    p.half_bits = scatter_half_bits(total);
+    p.n_qt = (int)n_qt;
+    p.by_qt = make_fastdiv((uint32_t)n_qt);
+    p.by_heads = make_fastdiv((uint32_t)a.heads);
+    p.by_arg = make_fastdiv(a.mask_kind == RAYA_MASK_BLOCKDIAG ? (uint32_t)a.mask_arg : 1u);
+    hipLaunchKernelGGL(attend_kernel<DP>, dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
     return hipGetLastError();
 }
 
