@@ -173,6 +173,58 @@ constexpr int kMinWaves = DP <= 64 ? 4 : DP == 128 ? 2 : 1;
 
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
+// The first tile's loads at head_dim 64, as one block the compiler cannot
+// split: 4 K DMAs (16 bytes per lane each, LDS address in m0), the lane's 4 Q
+// chunks into registers, 4 V DMAs, then a wait until only the V DMAs may be
+// outstanding (loads complete in issue order).  Written as one asm statement so
+// that the compiler neither waits for the V DMA before reading the K tile (it
+// cannot tell the two LDS tiles apart) nor touches q before the wait.
+__device__ __forceinline__ void issue_kqv64(const float *const ka[4], const uint32_t kl[4], const float *qa,
+                                            floatx4 q[4], const float *const va[4], const uint32_t vl[4]) {
+    asm volatile(
+        "s_mov_b32 m0, %[kl0]\n\tglobal_load_lds_dwordx4 %[ka0], off\n\t"
+        "s_mov_b32 m0, %[kl1]\n\tglobal_load_lds_dwordx4 %[ka1], off\n\t"
+        "s_mov_b32 m0, %[kl2]\n\tglobal_load_lds_dwordx4 %[ka2], off\n\t"
+        "s_mov_b32 m0, %[kl3]\n\tglobal_load_lds_dwordx4 %[ka3], off\n\t"
+        "global_load_dwordx4 %[q0], %[qa], off\n\t"
+        "global_load_dwordx4 %[q1], %[qa], off offset:16\n\t"
+        "global_load_dwordx4 %[q2], %[qa], off offset:32\n\t"
+        "global_load_dwordx4 %[q3], %[qa], off offset:48\n\t"
+        "s_mov_b32 m0, %[vl0]\n\tglobal_load_lds_dwordx4 %[va0], off\n\t"
+        "s_mov_b32 m0, %[vl1]\n\tglobal_load_lds_dwordx4 %[va1], off\n\t"
+        "s_mov_b32 m0, %[vl2]\n\tglobal_load_lds_dwordx4 %[va2], off\n\t"
+        "s_mov_b32 m0, %[vl3]\n\tglobal_load_lds_dwordx4 %[va3], off\n\t"
+        "s_waitcnt vmcnt(4)"
+        : [q0] "=&v"(q[0]), [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3])
+        : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [kl0] "s"(kl[0]),
+          [kl1] "s"(kl[1]), [kl2] "s"(kl[2]), [kl3] "s"(kl[3]), [qa] "v"(qa), [va0] "v"(va[0]),
+          [va1] "v"(va[1]), [va2] "v"(va[2]), [va3] "v"(va[3]), [vl0] "s"(vl[0]), [vl1] "s"(vl[1]),
+          [vl2] "s"(vl[2]), [vl3] "s"(vl[3])
+        : "memory", "m0");
+}
+
+// A later tile at head_dim 64: 4 K DMAs, 4 V DMAs, wait until only V may be
+// outstanding.
+__device__ __forceinline__ void issue_kv64(const float *const ka[4], const uint32_t kl[4],
+                                           const float *const va[4], const uint32_t vl[4]) {
+    asm volatile(
+        "s_mov_b32 m0, %[kl0]\n\tglobal_load_lds_dwordx4 %[ka0], off\n\t"
+        "s_mov_b32 m0, %[kl1]\n\tglobal_load_lds_dwordx4 %[ka1], off\n\t"
+        "s_mov_b32 m0, %[kl2]\n\tglobal_load_lds_dwordx4 %[ka2], off\n\t"
+        "s_mov_b32 m0, %[kl3]\n\tglobal_load_lds_dwordx4 %[ka3], off\n\t"
+        "s_mov_b32 m0, %[vl0]\n\tglobal_load_lds_dwordx4 %[va0], off\n\t"
+        "s_mov_b32 m0, %[vl1]\n\tglobal_load_lds_dwordx4 %[va1], off\n\t"
+        "s_mov_b32 m0, %[vl2]\n\tglobal_load_lds_dwordx4 %[va2], off\n\t"
+        "s_mov_b32 m0, %[vl3]\n\tglobal_load_lds_dwordx4 %[va3], off\n\t"
+        "s_waitcnt vmcnt(4)"
+        :
+        : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [kl0] "s"(kl[0]),
+          [kl1] "s"(kl[1]), [kl2] "s"(kl[2]), [kl3] "s"(kl[3]), [va0] "v"(va[0]), [va1] "v"(va[1]),
+          [va2] "v"(va[2]), [va3] "v"(va[3]), [vl0] "s"(vl[0]), [vl1] "s"(vl[1]), [vl2] "s"(vl[2]),
+          [vl3] "s"(vl[3])
+        : "memory", "m0");
+}
+
 // Workgroup barrier without the memory fence of __syncthreads: the fence would
 // wait for every outstanding LDS DMA (they count as LDS writes), including the
 // V tile that is meant to stay in flight during QK^T.  Callers order memory
@@ -201,9 +253,12 @@ __device__ __forceinline__ int swz(int c, int r) {
 // The body takes the K and V tiles as restrict pointers: inlined, that gives
 // their accesses distinct alias scopes, so the compiler knows the V tile's DMA
 // (still in flight during QK^T) does not write the K tile it reads.
-template <int DP>  // head_dim padded to a multiple of 16
+// FUSED (head_dim exactly 64): every tile's loads are issued by the asm blocks
+// above, so V stays in flight during QK^T and the softmax.
+template <int DP, bool FUSED>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs) {
+    static_assert(!FUSED || DP == 64, "the fused issue is written for head_dim 64");
     constexpr int DQ = DP / 4;   // head-dim slice owned by one lane group
     constexpr int NT = DP / 16;  // 16-dim output tiles
     constexpr int CH = DP / 4;   // 16-byte chunks per row
@@ -273,9 +328,35 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // clamped in-range address so all its loads are in flight together; the
     // out-of-range parts are zeroed after the wait), then V, which is only
     // waited for after QK^T and the softmax.
-    stage(kb, a.k_rs, ks, it.k_lo);
     float qreg[DQ];
-    {
+    // Operands of one tile's asm issue: this wave's K and V source rows and LDS slots.
+    const auto tile_addrs = [&](int kt, const float *ka[4], uint32_t kl[4], const float *va[4], uint32_t vl[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int slot = (wave * LPW + j) * 64 + lane;
+            const int r = slot / CH, c = swz<CH>(slot % CH, r);
+            const int64_t row = min(kt + r, min(kt + kKeys, it.k_hi) - 1);
+            ka[j] = kb + row * a.k_rs + 4 * c;
+            va[j] = vb + row * a.v_rs + 4 * c;
+            const int lds_off = (wave * LPW + j) * 64 * 16;
+            kl[j] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)((char *)ks + lds_off));
+            vl[j] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)((char *)vs + lds_off));
+        }
+    };
+    if constexpr (FUSED) {
+        // K, Q and V in one asm block that ends waiting for K and Q only.
+        const float *ka[4], *va[4];
+        uint32_t kl[4], vl[4];
+        tile_addrs(it.k_lo, ka, kl, va, vl);
+        const float *qa = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)min(qi, valid - 1) * a.q_rs + g * DQ;
+        floatx4 q4[4];
+        issue_kqv64(ka, kl, qa, q4, va, vl);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qreg[4 * c + e] = q4[c][e];
+    } else {
+        stage(kb, a.k_rs, ks, it.k_lo);
         const int qrow = min(qi, valid - 1);
         const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qrow * a.q_rs;
 #pragma unroll
@@ -286,8 +367,8 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             qreg[4 * c + 2] = x.z;
             qreg[4 * c + 3] = x.w;
         }
+        stage(vb, a.v_rs, vs, it.k_lo);
     }
-    stage(vb, a.v_rs, vs, it.k_lo);
 
     floatx4 oacc[NT];
 #pragma unroll
@@ -303,11 +384,19 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         if (kt != it.k_lo) {
             // The previous tile's LDS reads have returned (the MFMAs consumed them).
             barrier_only();
-            stage(kb, a.k_rs, ks, kt);
-            stage(vb, a.v_rs, vs, kt);
+            if constexpr (FUSED) {
+                const float *ka[4], *va[4];
+                uint32_t kl[4], vl[4];
+                tile_addrs(kt, ka, kl, va, vl);
+                issue_kv64(ka, kl, va, vl);
+            } else {
+                stage(kb, a.k_rs, ks, kt);
+                stage(vb, a.v_rs, vs, kt);
+            }
         }
-        __builtin_amdgcn_s_waitcnt(kWaitAllButV);  // this wave's K (and Q) loads have landed
-        barrier_only();                            // ... and every other wave's
+        // This wave's K (and Q) loads have landed (the fused issue waited already) ...
+        if constexpr (!FUSED) __builtin_amdgcn_s_waitcnt(kWaitAllButV);
+        barrier_only();  // ... and every other wave's
         if (kt == it.k_lo) {
             // Q is zero on rows at or beyond valid and on dims at or beyond D; a
             // negative scale is carried by negating Q.
@@ -428,11 +517,11 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     }
 }
 
-template <int DP>
+template <int DP, bool FUSED>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP>(a, p, ks, vs);
+    attend_body<DP, FUSED>(a, p, ks, vs);
 }
 
 // Half the bit width of the scatter domain: the smallest h with 4^h >= total.
@@ -442,7 +531,7 @@ int scatter_half_bits(int64_t total) {
     return h;
 }
 
-template <int DP>
+template <int DP, bool FUSED = false>
 hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const int64_t n_qt = (a.seq + kQRows - 1) / kQRows;
     const int64_t total = n_qt * a.heads * a.batch;
@@ -454,7 +543,7 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     p.by_qt = make_fastdiv((uint32_t)n_qt);
     p.by_heads = make_fastdiv((uint32_t)a.heads);
     p.by_arg = make_fastdiv(a.mask_kind == RAYA_MASK_BLOCKDIAG ? (uint32_t)a.mask_arg : 1u);
-    hipLaunchKernelGGL(attend_kernel<DP>, dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
+    hipLaunchKernelGGL((attend_kernel<DP, FUSED>), dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
     return hipGetLastError();
 }
 
@@ -466,7 +555,7 @@ hipError_t launch_attention(const AttnLaunch &a, hipStream_t stream) {
     case 16: return launch_dp<16>(a, stream);
     case 32: return launch_dp<32>(a, stream);
     case 48: return launch_dp<48>(a, stream);
-    case 64: return launch_dp<64>(a, stream);
+    case 64: return a.head_dim == 64 ? launch_dp<64, true>(a, stream) : launch_dp<64>(a, stream);
     case 80: return launch_dp<80>(a, stream);
     case 96: return launch_dp<96>(a, stream);
     case 112: return launch_dp<112>(a, stream);
