@@ -48,6 +48,43 @@ __device__ __forceinline__ float activate(float x) {
     else return x;
 }
 
+#ifndef GEMM_ORDER
+#define GEMM_ORDER 2
+#endif
+#ifndef GEMM_GROUP_M
+#define GEMM_GROUP_M 8
+#endif
+constexpr int kXcds = 8;
+#ifndef GEMM_USE_RING
+#define GEMM_USE_RING 1
+#endif
+constexpr bool kUseRing = GEMM_USE_RING;  // workgroup i runs on XCD i mod 8, each with its own L2
+
+// Output tile of workgroup `bid`.  Each XCD takes a contiguous range of the
+// tile sequence, and the sequence walks GROUP_M row blocks at a time, column
+// by column, so a B column tile is reused GROUP_M times and the A row blocks of
+// a group stay in that XCD's L2 while all of B streams past them.
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
+    int t = bid;
+    if (GEMM_ORDER >= 1) {
+        const int total = tiles_m * tiles_n;
+        const int per = total / kXcds, rem = total % kXcds;
+        const int xcd = bid % kXcds, slot = bid / kXcds;
+        t = xcd * per + min(xcd, rem) + slot;
+    }
+    if (GEMM_ORDER >= 2) {
+        const int width = GEMM_GROUP_M * tiles_n;
+        const int group = t / width, first = group * GEMM_GROUP_M;
+        const int size = min(tiles_m - first, GEMM_GROUP_M);
+        const int r = t - group * width;
+        tm = first + r % size;
+        tn = r / size;
+    } else {
+        tm = t / tiles_n;
+        tn = t % tiles_n;
+    }
+}
+
 // Loads 4 consecutive k values of row `row` (zero outside [0, rows) x [0, k)).
 template <bool VEC>
 __device__ __forceinline__ float4 load4(const float *base, int64_t ld, int row, int rows, int kcol,
@@ -65,6 +102,63 @@ __device__ __forceinline__ float4 load4(const float *base, int64_t ld, int row, 
     return x;
 }
 
+// Epilogue shared by both kernels.  Register r of acc[i][j] is row
+// wm + 32 i + 8 (r / 4) + 4 h + r % 4 and column wn + 32 j + li of the workgroup tile.
+template <int ACT, bool ROPE>
+__device__ __forceinline__ void epilogue(const GemmLaunch &g, const floatx16 (&acc)[2][2], int m0, int n0,
+                                         int wm, int wn, int li, int h) {
+    constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (row >= g.m) continue;
+            if constexpr (GEGLU) {
+                const int col = n0 + (wn >> 1) + li;
+                if (col >= g.n) continue;
+                float x = acc[i][0][r], gate = acc[i][1][r];
+                if (g.bias) {
+                    x += g.bias[col];
+                    gate += g.bias[g.n + col];
+                }
+                float y = gelu_erf(x) * gate;
+                if (g.residual) y += g.residual[(int64_t)row * g.ldr + col];
+                g.out[(int64_t)row * g.ldo + col] = y;
+            } else {
+                float y[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn + 32 * j + li;
+                    y[j] = acc[i][j][r];
+                    if (g.bias && col < g.n) y[j] += g.bias[col];
+                    y[j] = activate<ACT>(y[j]);
+                }
+                if constexpr (ROPE) {
+                    // Columns c and c + 32 of one 64-wide head sit in the same lane
+                    // and register of acc[i][0] and acc[i][1].
+                    const int col0 = n0 + wn + li;
+                    if (col0 < g.rope_cols) {
+                        const int64_t t = (int64_t)g.positions[row] * (kRopeHeadDim / 2) + li;
+                        const float c = g.rope_cos[t], sn = g.rope_sin[t];
+                        const float x0 = y[0], x1 = y[1];
+                        y[0] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+                        y[1] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, sn));
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int col = n0 + wn + 32 * j + li;
+                    if (col >= g.n) continue;
+                    float v = y[j];
+                    if (g.residual) v += g.residual[(int64_t)row * g.ldr + col];
+                    g.out[(int64_t)row * g.ldo + col] = v;
+                }
+            }
+        }
+    }
+}
+
 template <int ACT, bool VEC, bool ROPE>
 __global__ void __launch_bounds__(kThreads) gemm_nt_kernel(const GemmLaunch g) {
     __shared__ __attribute__((aligned(16))) float As[BM * SA];
@@ -74,7 +168,9 @@ __global__ void __launch_bounds__(kThreads) gemm_nt_kernel(const GemmLaunch g) {
     constexpr int OUT_BN = GEGLU ? BN / 2 : BN;  // output columns per workgroup
 
     const int tiles_n = (g.n + OUT_BN - 1) / OUT_BN;
-    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+    const int tiles_m = (g.m + BM - 1) / BM;
+    int tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * OUT_BN;
 
@@ -153,57 +249,120 @@ __global__ void __launch_bounds__(kThreads) gemm_nt_kernel(const GemmLaunch g) {
         }
     }
 
-    // Epilogue.  Register r of acc[i][j] is row wm + 32 i + 8 (r / 4) + 4 h + r % 4
-    // and column wn + 32 j + li of the workgroup tile.
+    epilogue<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h);
+}
+
+
+// The ring kernel: k a multiple of 16, 16-byte aligned operands with row
+// strides a multiple of 4 floats.  Slabs of 16 k go from HBM straight into a
+// 3-stage LDS ring (global_load_lds_dwordx4, no staging registers), two slabs
+// ahead of the MFMAs, with one barrier per slab.  The DMA is issued from asm
+// with explicit vmcnt waits: the compiler cannot tell the ring's stages apart
+// and would otherwise wait for every DMA before each LDS read.  Rows past m
+// (or past b's rows) load a clamped in-range row; the epilogue drops them.
+constexpr int RBK = 16;       // k per slab
+constexpr int RSTAGES = 3;    // LDS ring depth
+constexpr int kTileFloats = BM * RBK;  // one operand tile of one stage (8 KB)
+
+// 16-byte chunk c (0..3) of tile row r sits at chunk c ^ rswz(r) of the row:
+// the rows of any 8 or 16 consecutive lanes then cover every bank group.
+__device__ __forceinline__ int rswz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+typedef __attribute__((address_space(3))) void lds_ptr_t;
+
+__device__ __forceinline__ void dma16(const float *src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(src) : "memory", "m0");
+}
+
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int ACT, bool ROPE>
+__global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch g) {
+    __shared__ __attribute__((aligned(16))) float ring[RSTAGES * 2 * kTileFloats];  // 48 KB
+
+    constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
+    constexpr int OUT_BN = GEGLU ? BN / 2 : BN;
+    const int tiles_n = (g.n + OUT_BN - 1) / OUT_BN;
+    const int tiles_m = (g.m + BM - 1) / BM;
+    int tm, tn;
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * OUT_BN;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int li = lane & 31, h = lane >> 5;
+
+    // This thread's DMA sources: slot q = (2 wave + j) 64 + lane holds stored
+    // chunk q % 4 of tile row q / 4, i.e. data chunk (q % 4) ^ rswz(row).
+    const float *asrc[2], *bsrc[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
-            if (row >= g.m) continue;
-            if constexpr (GEGLU) {
-                const int col = n0 + (wn >> 1) + li;
-                if (col >= g.n) continue;
-                float x = acc[i][0][r], gate = acc[i][1][r];
-                if (g.bias) {
-                    x += g.bias[col];
-                    gate += g.bias[g.n + col];
-                }
-                float y = gelu_erf(x) * gate;
-                if (g.residual) y += g.residual[(int64_t)row * g.ldr + col];
-                g.out[(int64_t)row * g.ldo + col] = y;
-            } else {
-                float y[2];
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = n0 + wn + 32 * j + li;
-                    y[j] = acc[i][j][r];
-                    if (g.bias && col < g.n) y[j] += g.bias[col];
-                    y[j] = activate<ACT>(y[j]);
-                }
-                if constexpr (ROPE) {
-                    // Columns c and c + 32 of one 64-wide head sit in the same lane
-                    // and register of acc[i][0] and acc[i][1].
-                    const int col0 = n0 + wn + li;
-                    if (col0 < g.rope_cols) {
-                        const int64_t t = (int64_t)g.positions[row] * (kRopeHeadDim / 2) + li;
-                        const float c = g.rope_cos[t], sn = g.rope_sin[t];
-                        const float x0 = y[0], x1 = y[1];
-                        y[0] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
-                        y[1] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, sn));
-                    }
-                }
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int col = n0 + wn + 32 * j + li;
-                    if (col >= g.n) continue;
-                    float v = y[j];
-                    if (g.residual) v += g.residual[(int64_t)row * g.ldr + col];
-                    g.out[(int64_t)row * g.ldo + col] = v;
-                }
-            }
+    for (int j = 0; j < 2; ++j) {
+        const int q = (2 * wave + j) * 64 + lane;
+        const int row = q >> 2, c = (q & 3) ^ rswz(q >> 2);
+        asrc[j] = g.a + (int64_t)min(m0 + row, g.m - 1) * g.lda + 4 * c;
+        int brow;
+        if constexpr (GEGLU) {
+            // Tile rows [64t, 64t + 32) are input columns, [64t + 32, 64t + 64) their gates.
+            const int t = row >> 6, within = row & 63;
+            const int col = min(n0 + 32 * t + (within & 31), g.n - 1);
+            brow = within < 32 ? col : col + g.n;
+        } else {
+            brow = min(n0 + row, g.n_rows_b - 1);
         }
+        bsrc[j] = g.b + (int64_t)brow * g.ldb + 4 * c;
     }
+    const uint32_t ring_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)ring);
+    const auto issue = [&](int slab, int stage) {
+        const int k0 = slab * RBK;
+        const uint32_t sa = ring_base + (uint32_t)(stage * 2 * kTileFloats * 4);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dma16(asrc[j] + k0, sa + (2 * wave + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dma16(bsrc[j] + k0, sa + kTileFloats * 4 + (2 * wave + j) * 1024);
+    };
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nk = g.k / RBK;
+    issue(0, 0);
+    if (nk > 1) issue(1, 1);
+    int stage = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+        // Each wave issued 4 DMAs per slab: with slab kt + 1 in flight, vmcnt(4)
+        // means slab kt has landed; the barrier makes that hold for every wave and
+        // retires the reads of the stage slab kt + 2 goes into.
+        if (kt + 1 < nk)
+            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        barrier_only();
+        if (kt + 2 < nk) issue(kt + 2, stage == 0 ? 2 : stage - 1);
+        const float *As = ring + stage * 2 * kTileFloats, *Bs = As + kTileFloats;
+#pragma unroll
+        for (int kc = 0; kc < RBK / 4; kc += 2) {
+            float4 av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int ra = wm + 32 * i + li, rb = wn + 32 * i + li;
+                av[i] = *(const float4 *)&As[ra * RBK + 4 * ((kc + h) ^ rswz(ra))];
+                bv[i] = *(const float4 *)&Bs[rb * RBK + 4 * ((kc + h) ^ rswz(rb))];
+            }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(av[i][s], bv[j][s], acc[i][j]);
+        }
+        stage = stage == RSTAGES - 1 ? 0 : stage + 1;
+    }
+    epilogue<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h);
 }
 
 template <int ACT>
@@ -214,6 +373,19 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
     const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (((uintptr_t)g.a & 15) == 0) &&
                      (((uintptr_t)g.b & 15) == 0) && (g.k % 4 == 0);
     const dim3 grid((unsigned)tiles), block(kThreads);
+    const bool ring_ok = vec && g.k % RBK == 0 && g.k > 0;
+    if constexpr (ACT == RAYA_EPI_NONE) {
+        if (g.rope_cos && (g.rope_cols % kRopeHeadDim != 0 || g.rope_cols > g.n)) return hipErrorInvalidValue;
+    } else if (g.rope_cos) {
+        return hipErrorInvalidValue;
+    }
+    if (ring_ok && kUseRing) {
+        if (g.rope_cos)
+            hipLaunchKernelGGL((gemm_ring_kernel<ACT, ACT == RAYA_EPI_NONE>), grid, block, 0, stream, g);
+        else
+            hipLaunchKernelGGL((gemm_ring_kernel<ACT, false>), grid, block, 0, stream, g);
+        return hipGetLastError();
+    }
     if constexpr (ACT == RAYA_EPI_NONE) {
         if (g.rope_cos) {
             // The pairing (c, c + 32) needs 64-wide heads aligned to the 64-column wave tiles.

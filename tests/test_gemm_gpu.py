@@ -83,10 +83,12 @@ def _dev(x):
 
 @pytest.mark.parametrize("act", ["none", "gelu", "relu", "geglu"])
 @pytest.mark.parametrize("residual", [False, True])
-def test_device_epilogues(hip_gemm, act, residual):
-    """bias + activation (+ residual) against the oracle's matmul_nt and scalar ops."""
+@pytest.mark.parametrize("k", [136, 128])
+def test_device_epilogues(hip_gemm, act, residual, k):
+    """bias + activation (+ residual) against the oracle's matmul_nt and scalar ops, on both
+    kernels (k = 128: the LDS-ring kernel; k = 136: the general one)."""
     rng = np.random.default_rng(5)
-    m, n, k = 200, 96, 136
+    m, n = 200, 96
     rows_b = 2 * n if act == "geglu" else n
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = (0.1 * rng.standard_normal((rows_b, k))).astype(np.float32)
