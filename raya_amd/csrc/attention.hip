@@ -231,6 +231,9 @@ __device__ __forceinline__ void issue_kv64(const float *const ka[4], const uint3
 // themselves with explicit s_waitcnt; the clobber keeps the compiler from
 // moving memory operations across.
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+// A barrier after which other waves' direct loads overwrite LDS this wave has
+// read: its own LDS reads have returned first.
+__device__ __forceinline__ void barrier_after_reads() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Chunk (16 bytes) c of K/V row r sits at chunk swz(c, r) of the row in LDS:
 // an XOR swizzle within aligned groups of P chunks (P the largest power of two
@@ -241,6 +244,103 @@ template <int CH>
 __device__ __forceinline__ int swz(int c, int r) {
     constexpr int P = (CH & -CH) < 16 ? (CH & -CH) : 16;
     return (c & ~(P - 1)) | ((c ^ r) & (P - 1));
+}
+
+// S^T of one 64-key tile against this lane's Q slice: register (t, r) of lane
+// (g, li) becomes the raw score of key 16t + 4r + g of the tile (A-row i of
+// subtile t is key 16t + 4(i%4) + i/4, so row k_row0 = 4(li%4) + li/4).
+template <int DP>
+__device__ __forceinline__ void qk_tile(const float *ks, const float (&qreg)[DP / 4], int g, int k_row0,
+                                        floatx4 (&sacc)[4]) {
+    constexpr int DQ = DP / 4, CH = DP / 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        sacc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        const int row = 16 * t + k_row0;
+        const float *kp = ks + row * DP;
+#pragma unroll
+        for (int c = 0; c < DQ / 4; ++c) {
+            const float4 x = *(const float4 *)(kp + 4 * swz<CH>(g * (DQ / 4) + c, row));
+            sacc[t] = mfma(x.x, qreg[4 * c + 0], sacc[t]);
+            sacc[t] = mfma(x.y, qreg[4 * c + 1], sacc[t]);
+            sacc[t] = mfma(x.z, qreg[4 * c + 2], sacc[t]);
+            sacc[t] = mfma(x.w, qreg[4 * c + 3], sacc[t]);
+        }
+    }
+}
+
+// Masks scores outside [lo, hi) (tile-relative, already offset by g) when
+// need_mask, folds the tile into the running max m and partial sum l
+// (rescaling oacc unless first), and turns the scores into weights.
+template <int NT>
+__device__ __forceinline__ void softmax_tile(floatx4 (&sacc)[4], floatx4 (&oacc)[NT], float &m, float &l,
+                                             bool first, bool need_mask, int lo, int hi, float c_exp) {
+    if (need_mask) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int j = 16 * t + 4 * r;
+                if (j < lo || j >= hi) sacc[t][r] = -INFINITY;
+            }
+    }
+    float tmax = sacc[0][0];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[t][r]);
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m, tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    if (!first) {  // rescale what earlier tiles accumulated
+        const float alpha = fast_exp2((m - m_use) * c_exp);
+        l *= alpha;
+#pragma unroll
+        for (int n = 0; n < NT; ++n) oacc[n] *= alpha;
+    }
+    m = m_new;
+    // The difference is formed before scaling, so the terms that carry the
+    // weight (x near m) see no rounding from |x|.
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sacc[t][r] = fast_exp2((sacc[t][r] - m_use) * c_exp);
+            l += sacc[t][r];
+        }
+}
+
+// O^T += V^T P^T for one tile.  O^T tile n: A-row i is dim NT i + n, so one
+// lane reads NT contiguous floats of a V row for all n at once.
+template <int DP>
+__device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4], int g, int li,
+                                        floatx4 (&oacc)[DP / 16]) {
+    constexpr int NT = DP / 16, CH = DP / 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = 16 * t + 4 * r + g;
+            const float *vp = vs + row * DP;
+            float vop[NT];
+            if constexpr (NT == 4) {
+                const float4 x = *(const float4 *)(vp + 4 * swz<CH>(li, row));
+                vop[0] = x.x;
+                vop[1] = x.y;
+                vop[2] = x.z;
+                vop[3] = x.w;
+            } else {
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const int d = NT * li + n;
+                    vop[n] = vp[4 * swz<CH>(d >> 2, row) + (d & 3)];
+                }
+            }
+#pragma unroll
+            for (int n = 0; n < NT; ++n) oacc[n] = mfma(vop[n], sacc[t][r], oacc[n]);
+        }
+    }
 }
 
 // One workgroup computes one item.  Q goes straight to registers; each K/V
@@ -382,8 +482,8 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
 
     for (int kt = it.k_lo; kt < it.k_hi; kt += kKeys) {
         if (kt != it.k_lo) {
-            // The previous tile's LDS reads have returned (the MFMAs consumed them).
-            barrier_only();
+            // Every wave's LDS reads of the previous tile have returned.
+            barrier_after_reads();
             if constexpr (FUSED) {
                 const float *ka[4], *va[4];
                 uint32_t kl[4], vl[4];
@@ -410,90 +510,14 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         const bool active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
         floatx4 sacc[4];
         if (active) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sacc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-            const int row = 16 * t + k_row0;
-            const float *kp = ks + row * DP;
-#pragma unroll
-            for (int c = 0; c < DQ / 4; ++c) {
-                const float4 x = *(const float4 *)(kp + 4 * swz<CH>(g * (DQ / 4) + c, row));
-                sacc[t] = mfma(x.x, qreg[4 * c + 0], sacc[t]);
-                sacc[t] = mfma(x.y, qreg[4 * c + 1], sacc[t]);
-                sacc[t] = mfma(x.z, qreg[4 * c + 2], sacc[t]);
-                sacc[t] = mfma(x.w, qreg[4 * c + 3], sacc[t]);
-            }
-        }
-
-        // Register (t, r) of lane (g, li) is the raw score of key
-        // kt + 16t + 4r + g for query qi.
-        if (!(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi)) {
-            const int lo = rr.lo - kt - g, hi = rr.hi - kt - g;
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int j = 16 * t + 4 * r;
-                    if (j < lo || j >= hi) sacc[t][r] = -INFINITY;
-                }
-        }
-        float tmax = sacc[0][0];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[t][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const float m_new = fmaxf(m, tmax);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        if (kt != it.k_lo) {  // rescale what earlier tiles accumulated
-            const float alpha = fast_exp2((m - m_use) * c_exp);
-            l *= alpha;
-#pragma unroll
-            for (int n = 0; n < NT; ++n) oacc[n] *= alpha;
-        }
-        m = m_new;
-        // The difference is formed before scaling, so the terms that carry
-        // the weight (x near m) see no rounding from |x|.
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sacc[t][r] = fast_exp2((sacc[t][r] - m_use) * c_exp);
-                l += sacc[t][r];
-            }
-
+            qk_tile<DP>(ks, qreg, g, k_row0, sacc);
+            softmax_tile<NT>(sacc, oacc, m, l, kt == it.k_lo,
+                             !(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi), rr.lo - kt - g,
+                             rr.hi - kt - g, c_exp);
         }
         __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's V loads have landed
         barrier_only();
-        if (!active) continue;
-
-        // O^T tile n: A-row i is dim NT i + n, so one lane reads NT contiguous
-        // floats of a V row for all n at once.
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * t + 4 * r + g;
-                const float *vp = vs + row * DP;
-                float vop[NT];
-                if constexpr (NT == 4) {
-                    const float4 x = *(const float4 *)(vp + 4 * swz<CH>(li, row));
-                    vop[0] = x.x;
-                    vop[1] = x.y;
-                    vop[2] = x.z;
-                    vop[3] = x.w;
-                } else {
-#pragma unroll
-                    for (int n = 0; n < NT; ++n) {
-                        const int d = NT * li + n;
-                        vop[n] = vp[4 * swz<CH>(d >> 2, row) + (d & 3)];
-                    }
-                }
-#pragma unroll
-                for (int n = 0; n < NT; ++n) oacc[n] = mfma(vop[n], sacc[t][r], oacc[n]);
-            }
-        }
+        if (active) pv_tile<DP>(vs, sacc, g, li, oacc);
     }
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
