@@ -32,23 +32,60 @@ PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
 METRIC = "fp32 block-local attn TFLOP/s + % roofline; encoder sequences/sec, 1 GPU"
 
+def _attn(config, batch, heads, seq, mask, valid, outliers=False, data="normal"):
+    return {"config": config, "batch": batch, "heads": heads, "seq": seq, "head_dim": 64,
+            "mask": mask, "valid": valid, "outliers": outliers, "data": data}
+
+
 WORKLOADS = {
-    # name: (workload number for seeds, batch, heads, seq, head_dim, block, valid range, outliers)
-    "attn_b32_h12_l2048_d64_blockdiag64": (2, 32, 12, 2048, 64, 64, (512, 2048), False),
-    "attn_b1_h12_l512_d64_blockdiag64": (1, 1, 12, 512, 64, 64, (512, 512), False),
-    "attn_b4_h12_l16384_d64_blockdiag128": (5, 4, 12, 16384, 64, 128, (8192, 16384), True),
+    # BlockDiag(b): each query sees its own b-token block (the default line and its configs)
+    "attn_b32_h12_l2048_d64_blockdiag64": _attn(2, 32, 12, 2048, ("block_diag", 64), (512, 2048)),
+    "attn_b1_h12_l512_d64_blockdiag64": _attn(1, 1, 12, 512, ("block_diag", 64), (512, 512)),
+    "attn_b4_h12_l16384_d64_blockdiag128": _attn(5, 4, 12, 16384, ("block_diag", 128), (8192, 16384),
+                                                 outliers=True),
+    # the reference's own masks at the same shapes: Block3 = own 128-block and both neighbours
+    "attn_b32_h12_l2048_d64_block3": _attn(2, 32, 12, 2048, ("block3",), (512, 2048)),
+    "attn_b1_h12_l512_d64_block3": _attn(1, 1, 12, 512, ("block3",), (512, 512)),
+    "attn_b4_h12_l16384_d64_block3": _attn(5, 4, 12, 16384, ("block3",), (8192, 16384), outliers=True),
+    # the reference bench's shapes and inputs (16 heads, one sequence, no padding, xorshift
+    # U[-1, 1] from seeds 42/43/44; benches/local_attention.rs:21-22, 90-97)
+    **{f"refbench_h16_l{n}_d64_{m}": _attn(0, 1, 16, n, (m,), (n, n), data="xorshift")
+       for n in (2048, 4096, 8192) for m in ("block3", "window64")},
 }
 DEFAULT = "attn_b32_h12_l2048_d64_blockdiag64"
+REF_BLOCK, REF_WINDOW = 128, 64
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def algorithmic(valid, heads, head_dim, seq, block):
+def mask_name(mask) -> str:
+    return f"block_diag({mask[1]})" if mask[0] == "block_diag" else mask[0]
+
+
+def key_pairs(mask, v: int) -> int:
+    """Sum over rows i < v of |key_range(i, v)| (attention.rs:48-59, plus BlockDiag(b))."""
+    import numpy as np
+
+    if mask[0] == "block_diag":
+        b = mask[1]
+        return b * b * (v // b) + (v % b) ** 2
+    i = np.arange(v, dtype=np.int64)
+    if mask[0] == "block3":
+        blk = i // REF_BLOCK
+        lo, hi = np.maximum(blk - 1, 0) * REF_BLOCK, (blk + 2) * REF_BLOCK
+    elif mask[0] == "window64":
+        lo, hi = np.maximum(i - REF_WINDOW, 0), i + REF_WINDOW + 1
+    else:
+        raise ValueError(mask)
+    return int((np.minimum(hi, v) - np.minimum(lo, v)).sum())
+
+
+def algorithmic(valid, heads, head_dim, seq, mask):
     """FLOP = 4 D H sum_b sum_{i<v_b} |keys(i)|; bytes = Q, K, V valid rows read once + all
     output rows written (fp32)."""
-    keys = sum(block * block * (int(v) // block) + (int(v) % block) ** 2 for v in valid)
+    keys = sum(key_pairs(mask, int(v)) for v in valid)
     flops = 4 * head_dim * heads * keys
     nbytes = 4 * (3 * heads * head_dim * int(sum(int(v) for v in valid))
                   + len(valid) * heads * seq * head_dim)
@@ -60,15 +97,22 @@ def make_inputs(wl):
 
     from raya_amd import synth
 
-    c, b, h, s, d, block, (lo, hi), outliers = wl
+    c, b, h, s, d = wl["config"], wl["batch"], wl["heads"], wl["seq"], wl["head_dim"]
+    lo, hi = wl["valid"]
     n = b * h * s * d
     qkv = []
     for i in range(3):
-        x = synth.normal(synth.workload_seed(c, i), n).reshape(b, h, s, d)
-        if outliers:
+        if wl["data"] == "xorshift":
+            x = synth.xorshift_uniform(42 + i, n).reshape(b, h, s, d)
+        else:
+            x = synth.normal(synth.workload_seed(c, i), n).reshape(b, h, s, d)
+        if wl["outliers"]:
             synth.with_outliers(x, synth.workload_seed(c, 4) + 10 * i)
         qkv.append(x)
-    valid = synth.integers(synth.workload_seed(c, 3), b, lo, hi).astype(np.int32)
+    if lo == hi:
+        valid = np.full(b, lo, np.int32)
+    else:
+        valid = synth.integers(synth.workload_seed(c, 3), b, lo, hi).astype(np.int32)
     return qkv, valid
 
 
@@ -76,29 +120,31 @@ def cpu_baseline(qkv, valid, wl, budget_s: float):
     """The reference's Tiled algorithm (AVX2+FMA when present) on this host's cores."""
     import oracle
 
-    c, b, h, s, d, block, _, _ = wl
+    b, h, s, d, mask = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"], wl["mask"]
+    kind = {"block_diag": oracle.MASK_BLOCKDIAG, "block3": oracle.MASK_BLOCK3,
+            "window64": oracle.MASK_WINDOW64}[mask[0]]
+    block = mask[1] if mask[0] == "block_diag" else REF_BLOCK
     threads = min(16, len(os.sched_getaffinity(0)))
     q, k, v = qkv
     backend = 1 if oracle.cpu_has_avx2_fma() else 0
-    flops, _ = algorithmic(valid, h, d, s, block)
+    flops, _ = algorithmic(valid, h, d, s, mask)
     times = []
     out = None
     t_end = time.perf_counter() + budget_s
     while True:
         t0 = time.perf_counter()
-        out, used = oracle.tiled_attend_batched(q, k, v, oracle.MASK_BLOCKDIAG, valid, 0.125,
-                                                block=block, threads=threads, backend=backend,
-                                                out=out)
+        out, used = oracle.tiled_attend_batched(q, k, v, kind, valid, 0.125, block=block,
+                                                threads=threads, backend=backend, out=out)
         times.append(time.perf_counter() - t0)
         if time.perf_counter() > t_end or len(times) >= 50:
             break
     med = statistics.median(times)
     # single-thread figure on the first sequences (the reference bench's t1 leg)
     n1 = max(1, min(b, 4))
-    f1, _ = algorithmic(valid[:n1], h, d, s, block)
+    f1, _ = algorithmic(valid[:n1], h, d, s, mask)
     t0 = time.perf_counter()
-    oracle.tiled_attend_batched(q[:n1], k[:n1], v[:n1], oracle.MASK_BLOCKDIAG, valid[:n1], 0.125,
-                                block=block, threads=1, backend=backend)
+    oracle.tiled_attend_batched(q[:n1], k[:n1], v[:n1], kind, valid[:n1], 0.125, block=block,
+                                threads=1, backend=backend)
     t1 = time.perf_counter() - t0
     return out, {
         "value": flops / med / 1e12,
@@ -255,7 +301,8 @@ def main() -> int:
     import raya_amd as R
 
     wl = WORKLOADS[args.workload]
-    c, b, h, s, d, block, (lo, hi), outliers = wl
+    b, h, s, d, mask_spec = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"], wl["mask"]
+    lo, hi = wl["valid"]
     log(f"generating inputs for {args.workload}")
     qkv, valid = make_inputs(wl)
     dev = torch.device("cuda:0")
@@ -263,9 +310,10 @@ def main() -> int:
     vl = torch.from_numpy(valid).to(dev)
     out = torch.empty_like(q)
     kernel = R.HipAttention()
-    mask = R.Mask.block_diag(block)
+    mask = {"block_diag": lambda: R.Mask.block_diag(mask_spec[1]), "block3": lambda: R.Mask.BLOCK3,
+            "window64": lambda: R.Mask.WINDOW64}[mask_spec[0]]()
     stream = torch.cuda.current_stream(dev)
-    flops, nbytes = algorithmic(valid, h, d, s, block)
+    flops, nbytes = algorithmic(valid, h, d, s, mask_spec)
 
     def step():
         kernel.attend_batched(q, k, v, out, vl, mask, stream=stream)
@@ -305,20 +353,30 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": args.workload, "batch": b, "heads": h, "seq": s, "head_dim": d,
-                   "mask": f"block_diag({block})", "valid_len": f"uniform [{lo}, {hi}]",
-                   "outliers": "1% x20" if outliers else "none", "flop_per_step": flops,
+                   "mask": mask_name(mask_spec),
+                   "valid_len": f"uniform [{lo}, {hi}]" if lo != hi else f"{lo} (no padding)",
+                   "inputs": ("xorshift U[-1, 1], seeds 42/43/44" if wl["data"] == "xorshift"
+                              else "N(0, 1), SplitMix64 + Box-Muller"),
+                   "outliers": "1% x20" if wl["outliers"] else "none", "flop_per_step": flops,
                    "bytes_per_step": nbytes},
         "kernel_ms": avg_kernel_s * 1e3,
         "kernel_tflops": flops / avg_kernel_s / 1e12,
         "mfma_frac": flops / avg_kernel_s / 1e12 / PEAK_FP32_MFMA_TFLOPS,
     }
-    achieved = nbytes / avg_kernel_s / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", f"{args.workload}_traffic.json")
     if os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
-    result["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
-                          "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": traffic}
+    # The bound is the one the arithmetic intensity reaches first.
+    if flops / nbytes < PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
+        achieved = nbytes / avg_kernel_s / 1e9
+        result["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
+                              "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": traffic}
+    else:
+        achieved = flops / avg_kernel_s / 1e12
+        result["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS,
+                              "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
+                              "traffic": traffic}
 
     if not args.no_cpu_baseline:
         log("cpu baseline")

@@ -68,3 +68,73 @@ def with_outliers(x: np.ndarray, seed: int, p: float = 0.01, factor: float = 20.
 
 def workload_seed(config: int, stream: int) -> int:
     return 1000 * config + stream
+
+
+# ---------------------------------------------------------------------------
+# The reference bench's inputs: xorshift64 (shifts 13, 7, 17) seeded with
+# seed * 0x9E3779B97F4A7C15 | 1; each value is the top 24 bits of the state
+# after a step, as u / 2^24, mapped to 2u - 1 in [-1, 1)
+# (crates/raya-kernels/tests/common/mod.rs:6-18; q, k, v use seeds 42, 43, 44
+# in benches/local_attention.rs:95).
+#
+# One xorshift step is linear over GF(2)^64, so the sequence is produced in
+# parallel: `lanes` independent states start `chunk` steps apart (state
+# advanced with T^chunk, T the step's 64x64 bit matrix) and all lanes step
+# together with vectorised numpy.
+
+_MASK64 = (1 << 64) - 1
+
+
+def _xs_step(s: int) -> int:
+    s ^= (s << 13) & _MASK64
+    s ^= s >> 7
+    s ^= (s << 17) & _MASK64
+    return s
+
+
+def _apply(cols, s: int) -> int:
+    """Bit matrix (column j = image of bit j) applied to state s."""
+    r = 0
+    j = 0
+    while s:
+        if s & 1:
+            r ^= cols[j]
+        s >>= 1
+        j += 1
+    return r
+
+
+def _power(cols, e: int):
+    """Columns of the matrix raised to the power e."""
+    result = [1 << j for j in range(64)]
+    base = list(cols)
+    while e:
+        if e & 1:
+            result = [_apply(base, c) for c in result]
+        base = [_apply(base, c) for c in base]
+        e >>= 1
+    return result
+
+
+def xorshift_uniform(seed: int, n: int, lanes: int = 4096) -> np.ndarray:
+    """n values of the reference bench's generator, as float32 in [-1, 1)."""
+    if n <= 0:
+        return np.empty(0, dtype=np.float32)
+    s0 = ((seed * 0x9E3779B97F4A7C15) & _MASK64) | 1
+    lanes = max(1, min(lanes, n))
+    chunk = (n + lanes - 1) // lanes
+    step = [_xs_step(1 << j) for j in range(64)]
+    jump = _power(step, chunk)
+    starts = [s0]
+    for _ in range(lanes - 1):
+        starts.append(_apply(jump, starts[-1]))
+    s = np.array(starts, dtype=np.uint64)
+    vals = np.empty((chunk, lanes), dtype=np.float32)
+    with np.errstate(over="ignore"):
+        for i in range(chunk):
+            s ^= s << np.uint64(13)
+            s ^= s >> np.uint64(7)
+            s ^= s << np.uint64(17)
+            vals[i] = (s >> np.uint64(40)).astype(np.float32)
+    u = vals.T.reshape(-1)[:n] * np.float32(1.0 / (1 << 24))
+    return np.float32(2.0) * u - np.float32(1.0)
