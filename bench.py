@@ -14,7 +14,10 @@ Tiled CPU algorithm timed on this host on the same inputs.
 With the default workload the line also carries "encoder": sequences/sec of the
 full 12-layer ModernBERT-base decision-model forward (B=64, L=512, valid
 lengths uniform in [128, 512], random N(0, 0.02) weights from a safetensors
-checkpoint) and the oracle's CPU forward on the first sequences beside it.
+checkpoint) and the oracle's CPU forward on the first sequences beside it, and
+"encoder_layer": one block-local layer of that model on B=16 x L=1024 valid
+tokens (BlockDiag(64) on the local layers), from the forward's own per-layer
+event spans.
 """
 from __future__ import annotations
 
@@ -167,6 +170,14 @@ ENCODER = {
 }
 
 
+LAYER = {
+    # one local (block-local) layer of the same model on 16 sequences of 1024 valid tokens
+    "workload": "encoder_layer_b16_l1024_768_geglu_blockdiag64",
+    "config": 3, "batch": 16, "seq": 1024, "valid": (1024, 1024), "cls_id": 101,
+    "ids": (1000, 30522), "markers": [1, 2], "qtype": 0, "block": 64,
+}
+
+
 def encoder_flops(valid, d=768, inter=3072, heads=12, layers=12, global_every=3, window=64):
     """GEMM FLOP on valid tokens (2 d (3d + d + 2F + F) per token and layer, GeGLU Wi is
     [2F, d]) plus attention FLOP (4 D H per allowed (query, key) pair; Full on global layers,
@@ -203,7 +214,7 @@ def encoder_inputs(spec):
     return ids, valid, pos, mask, qtype
 
 
-def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dict:
+def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool, layer: bool = True) -> dict:
     """Sequences/sec of the full forward (embed, 12 layers, final norm, scorer, act head) on a
     batch of 64; each step includes the input upload, every kernel, the output download and
     the stream synchronisation."""
@@ -243,6 +254,8 @@ def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dic
             "steps": steps, "warmup": warmup,
             "act_logits_finite": bool(np.isfinite(out.act_logits).all()),
         }
+        if layer:
+            res["layer"] = bench_layer(m, steps, warmup)
         if cpu:
             log("encoder: cpu baseline")
             res["cpu_baseline"] = encoder_cpu_baseline(tmp, ids, valid, pos, mask, qtype, out,
@@ -250,6 +263,59 @@ def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dic
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     return res
+
+
+def bench_layer(m, steps: int, warmup: int) -> dict:
+    """One block-local encoder layer (pre-LN, QKV + RoPE, BlockDiag(64) attention, Wo + residual,
+    LN, GeGLU, Wo + residual) on B=16 x L=1024 valid tokens: the per-layer event spans of the
+    model's own forward (stage timing level 1), median over the local layers and steps; a level-2
+    forward gives the per-kernel split."""
+    import numpy as np
+
+    from raya_amd import Mask
+
+    spec = LAYER
+    ids, valid, pos, mask, qtype = encoder_inputs(spec)
+    info = m.info
+    n_layers, every = info["num_hidden_layers"], info["global_attn_every_n_layers"]
+    local = [i for i in range(n_layers) if i % every != 0]
+    lm = Mask.block_diag(spec["block"])
+    log(f"layer: warmup {warmup}, timing {steps} forwards (B={spec['batch']}, L={spec['seq']})")
+    m.set_profiling(1)
+    try:
+        for _ in range(warmup):
+            m.forward_batch(ids, valid, pos, mask, qtype, local_mask=lm)
+        times = []
+        for _ in range(steps):
+            m.forward_batch(ids, valid, pos, mask, qtype, local_mask=lm)
+            st = dict(m.stage_times())
+            times += [st[f"encoder_layer_{i:02d}"] for i in local]
+        m.set_profiling(2)
+        m.forward_batch(ids, valid, pos, mask, qtype, local_mask=lm)
+        st2 = m.stage_times()
+    finally:
+        m.set_profiling(0)
+    ms = statistics.median(times)
+    tokens = int(valid.sum())
+    d, inter, heads = info["hidden_size"], info["intermediate_size"], info["num_attention_heads"]
+    hd = d // heads
+    gemm = tokens * 2 * d * (3 * d + d + 2 * inter + inter)
+    b = spec["block"]
+    attn = 4 * hd * heads * sum(b * b * (int(v) // b) + (int(v) % b) ** 2 for v in valid)
+    ops = {}
+    for name, t in st2:
+        if "/" in name and int(name.split("/")[0].rsplit("_", 1)[1]) in local:
+            ops.setdefault(name.split("/")[1], []).append(t)
+    return {
+        "workload": spec["workload"], "batch": spec["batch"], "seq": spec["seq"],
+        "valid_tokens": tokens, "mask": f"block_diag({b}) (local layers)",
+        "ms_per_layer": ms, "sequences_per_s": spec["batch"] / (ms / 1e3),
+        "flop_per_layer": gemm + attn, "tflops": (gemm + attn) / (ms / 1e3) / 1e12,
+        "mfma_frac": (gemm + attn) / (ms / 1e3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+        "timing": f"median of {len(times)} local-layer spans ({len(local)} layers x {steps} forwards)",
+        "kernels_ms": {k: statistics.mean(v) for k, v in ops.items()},
+        "layer_input": "normalised token embeddings of uniform random ids (unit variance rows)",
+    }
 
 
 def encoder_cpu_baseline(ckpt, ids, valid, pos, mask, qtype, gpu_out, budget_s: float) -> dict:
@@ -388,8 +454,12 @@ def main() -> int:
         cb["gpu_vs_cpu_max_abs"] = diff
         result["cpu_baseline"] = cb
     if args.workload == DEFAULT and not args.no_encoder:
-        result["encoder"] = bench_encoder(args.encoder_steps, args.encoder_warmup, args.cpu_seconds,
-                                          cpu=not args.no_cpu_baseline)
+        enc = bench_encoder(args.encoder_steps, args.encoder_warmup, args.cpu_seconds,
+                            cpu=not args.no_cpu_baseline)
+        layer = enc.pop("layer", None)
+        result["encoder"] = enc
+        if layer is not None:
+            result["encoder_layer"] = layer
     print(json.dumps(result), flush=True)
     return 0
 

@@ -239,6 +239,25 @@ typedef void (*raya_trace_fn)(void *user, const char *name, const uint64_t *shap
 int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_forward_output *out,
                        raya_trace_fn trace, void *user, void *stream);
 
+/* Stage timing, the forward's counterpart of Tiled::attend_with_stages
+ * (crates/raya-kernels/src/tiled/mod.rs:61-126): with level 1,
+ * raya_model_forward records a HIP event pair on its stream around the
+ * embedding, each encoder layer, the final norm, each head layer and the
+ * scorer + act head; with level 2 also around every kernel of an encoder layer
+ * ("encoder_layer_03/qkv", "/attention", "/attn_out", "/mlp_norm",
+ * "/mlp_in_geglu", "/mlp_out", "/attn_norm").  Level 0 (the default) records
+ * nothing.  raya_model_stage_times returns the last forward's spans in order:
+ * min(capacity, count) entries, *count the full number.  Spans that contain a
+ * trace callback include its host copies. */
+int raya_model_set_profiling(raya_model *model, int level);
+
+typedef struct raya_stage_time {
+    char name[48];
+    double ms;
+} raya_stage_time;
+
+int raya_model_stage_times(raya_model *model, raya_stage_time *out, uint64_t capacity, uint64_t *count);
+
 #ifdef __cplusplus
 }
 #endif

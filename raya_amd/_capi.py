@@ -78,6 +78,10 @@ class ForwardOutputC(ctypes.Structure):
                 ("logits", "probabilities", "act_logits", "features", "pooled")]
 
 
+class StageTimeC(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 48), ("ms", ctypes.c_double)]
+
+
 TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p,
                             ctypes.POINTER(ctypes.c_uint64), ctypes.c_uint32,
                             ctypes.POINTER(ctypes.c_float))
@@ -105,6 +109,9 @@ SIGNATURES = [
     ("raya_model_get_info", ctypes.c_int, [_vp, ctypes.POINTER(ModelInfoC)]),
     ("raya_model_forward", ctypes.c_int, [_vp, ctypes.POINTER(ForwardBatchC),
                                           ctypes.POINTER(ForwardOutputC), TRACE_FN, _vp, _vp]),
+    ("raya_model_set_profiling", ctypes.c_int, [_vp, ctypes.c_int]),
+    ("raya_model_stage_times", ctypes.c_int, [_vp, ctypes.POINTER(StageTimeC), _u64,
+                                              ctypes.POINTER(_u64)]),
 ]
 
 _lib = None

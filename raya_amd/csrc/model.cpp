@@ -587,6 +587,8 @@ struct Model {
     Weights w;
     std::mutex mu;
     std::unordered_map<int, std::unique_ptr<DeviceModel>> dev;
+    int profile = 0;                                    // stage timing level (0: off)
+    std::vector<std::pair<std::string, double>> stages;  // the last forward's stage times, ms
 };
 
 namespace {
@@ -714,6 +716,29 @@ int raya_model_get_info(const raya_model *model, raya_model_info *info) {
     info->head_ffn = c.head_ffn;
     info->n_act = c.n_act;
     info->param_floats = ((const Model *)model)->w.host.size();
+    return ok();
+}
+
+int raya_model_set_profiling(raya_model *model, int level) {
+    if (!model) return fail(RAYA_ERR_INPUT, "invalid input: null model");
+    if (level < 0 || level > 2) return fail(RAYA_ERR_INPUT, "invalid input: profiling level must be 0, 1 or 2");
+    Model &m = *(Model *)model;
+    std::lock_guard<std::mutex> lock(m.mu);
+    m.profile = level;
+    m.stages.clear();
+    return ok();
+}
+
+int raya_model_stage_times(raya_model *model, raya_stage_time *out, uint64_t capacity, uint64_t *count) {
+    if (!model || !count) return fail(RAYA_ERR_INPUT, "invalid input: null model or count");
+    Model &m = *(Model *)model;
+    std::lock_guard<std::mutex> lock(m.mu);
+    *count = m.stages.size();
+    for (uint64_t i = 0; i < m.stages.size() && i < capacity && out; ++i) {
+        memset(out[i].name, 0, sizeof out[i].name);
+        strncpy(out[i].name, m.stages[i].first.c_str(), sizeof out[i].name - 1);
+        out[i].ms = m.stages[i].second;
+    }
     return ok();
 }
 
@@ -888,6 +913,44 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         if (r_) return r_;  \
     } while (0)
 
+    // Stage timing: an event pair on the stream around each span whose level is
+    // at most the model's profiling level; read back after the final sync.
+    struct Span {
+        std::string name;
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+    };
+    struct Spans {
+        std::vector<Span> v;
+        ~Spans() {
+            for (auto &s : v) {
+                if (s.e0) (void)hipEventDestroy(s.e0);
+                if (s.e1) (void)hipEventDestroy(s.e1);
+            }
+        }
+    } spans;
+    const int profile = m.profile;
+    m.stages.clear();
+    auto span_begin = [&](int level, const std::string &nm, int *idx) -> int {
+        *idx = -1;
+        if (profile < level) return RAYA_OK;
+        Span sp;
+        sp.name = nm;
+        TRY_HIP(hipEventCreate(&sp.e0), "stage event");
+        spans.v.push_back(sp);
+        TRY_HIP(hipEventCreate(&spans.v.back().e1), "stage event");
+        TRY_HIP(hipEventRecord(spans.v.back().e0, stream), "stage event");
+        *idx = (int)spans.v.size() - 1;
+        return RAYA_OK;
+    };
+    auto span_end = [&](int idx) -> int {
+        if (idx < 0) return RAYA_OK;
+        TRY_HIP(hipEventRecord(spans.v[idx].e1, stream), "stage event");
+        return RAYA_OK;
+    };
+    int sp_stage = -1, sp_op = -1;
+#define SPAN(level, nm, slot) RECORD(span_begin(level, nm, &slot))
+#define SPAN_END(slot) RECORD(span_end(slot))
+
     auto P = [&](const std::string &name) { return param(m, dm, name); };
     auto gemm = [&](float *o, int64_t ldo, const float *a, int64_t lda, const float *wt, uint64_t rows, uint64_t n,
                     uint64_t k, int act, const float *bias, const float *res) -> int {
@@ -959,17 +1022,25 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     const float *rope_t = (const float *)dm.rope.ptr;
 
     // encoder::embed (encoder.rs:15-32)
+    SPAN(1, "embedding", sp_stage);
     RECORD(layer_norm(P("encoder.embeddings.tok_embeddings.weight"), d_ids, P("encoder.embeddings.norm.weight"),
                       nullptr, eps, T, h, nullptr, nullptr));
+    SPAN_END(sp_stage);
     RECORD(record_rows("embedding_output", h, d));
     char name[64];
     for (uint64_t i = 0; i < c.layers; ++i) {
         const std::string p = "encoder.layers." + std::to_string(i);
+        snprintf(name, sizeof name, "encoder_layer_%02d", (int)i);
+        const std::string sn = name;
+        SPAN(1, sn, sp_stage);
         const float *x = h;
         if (i > 0) {
+            SPAN(2, sn + "/attn_norm", sp_op);
             RECORD(layer_norm(h, nullptr, P(p + ".attn_norm.weight"), nullptr, eps, T, nb, nullptr, nullptr));
+            SPAN_END(sp_op);
             x = nb;
         }
+        SPAN(2, sn + "/qkv", sp_op);
         const bool global = c.is_global(i);
         const float *cos_t = rope_t + (global ? 0 : 2) * rope_one, *sin_t = cos_t + rope_one;
         if (hd == (uint64_t)kRopeHeadDim) {
@@ -994,18 +1065,31 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
             RECORD(gemm(qkv, 3 * d, x, d, P(p + ".attn.Wqkv.weight"), T, 3 * d, d, RAYA_EPI_NONE, nullptr, nullptr));
             TRY_HIP(launch_rope(qkv, (int64_t)(3 * d), d_pos, cos_t, sin_t, (int)T, (int)d, (int)hd, stream), "rope");
         }
+        SPAN_END(sp_op);
+        SPAN(2, sn + "/attention", sp_op);
         if (global) RECORD(attend(qkv, c.heads, hd, RAYA_MASK_FULL, 0));
         else RECORD(attend(qkv, c.heads, hd, local_kind, local_arg));
+        SPAN_END(sp_op);
+        SPAN(2, sn + "/attn_out", sp_op);
         RECORD(gemm(h, d, ctx, d, P(p + ".attn.Wo.weight"), T, d, d, RAYA_EPI_NONE, nullptr, h));
+        SPAN_END(sp_op);
+        SPAN(2, sn + "/mlp_norm", sp_op);
         RECORD(layer_norm(h, nullptr, P(p + ".mlp_norm.weight"), nullptr, eps, T, nb, nullptr, nullptr));
+        SPAN_END(sp_op);
+        SPAN(2, sn + "/mlp_in_geglu", sp_op);
         RECORD(gemm(gated, inter, nb, d, P(p + ".mlp.Wi.weight"), T, inter, d, RAYA_EPI_GEGLU, nullptr, nullptr));
+        SPAN_END(sp_op);
+        SPAN(2, sn + "/mlp_out", sp_op);
         RECORD(gemm(h, d, gated, inter, P(p + ".mlp.Wo.weight"), T, d, inter, RAYA_EPI_NONE, nullptr, h));
-        snprintf(name, sizeof name, "encoder_layer_%02d", (int)i);
-        RECORD(record_rows(name, h, d));
+        SPAN_END(sp_op);
+        SPAN_END(sp_stage);
+        RECORD(record_rows(sn.c_str(), h, d));
     }
     // final norm, then + type_emb[qtype] (model.rs:283-304); nb holds the normed rows
+    SPAN(1, "final_norm", sp_stage);
     RECORD(layer_norm(h, nullptr, P("encoder.final_norm.weight"), nullptr, eps, T, trace ? nb : nullptr,
                       P("type_emb.weight"), h));
+    SPAN_END(sp_stage);
     if (trace) {
         RECORD(record_rows("encoder_final_norm", nb, d));
         RECORD(record_rows("encoder_output", nb, d));
@@ -1019,6 +1103,8 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     // head layers: nn.TransformerEncoderLayer(norm_first=True) (head.rs:14-48)
     for (uint64_t i = 0; i < c.head_layers; ++i) {
         const std::string p = "head.layers." + std::to_string(i);
+        snprintf(name, sizeof name, "head_layer_%02d", (int)i);
+        SPAN(1, name, sp_stage);
         RECORD(layer_norm(h, nullptr, P(p + ".norm1.weight"), P(p + ".norm1.bias"), head_eps, T, nb, nullptr, nullptr));
         RECORD(gemm(qkv, 3 * d, nb, d, P(p + ".self_attn.in_proj_weight"), T, 3 * d, d, RAYA_EPI_NONE,
                     P(p + ".self_attn.in_proj_bias"), nullptr));
@@ -1030,10 +1116,11 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
                     P(p + ".linear1.bias"), nullptr));
         RECORD(gemm(h, d, gated, c.head_ffn, P(p + ".linear2.weight"), T, d, c.head_ffn, RAYA_EPI_NONE,
                     P(p + ".linear2.bias"), h));
-        snprintf(name, sizeof name, "head_layer_%02d", (int)i);
+        SPAN_END(sp_stage);
         RECORD(record_rows(name, h, d));
     }
     // marker scorer (head.rs:50-67), then the per-sequence tail
+    SPAN(1, "scorer_and_act_head", sp_stage);
     TRY_HIP(launch_gather_rows(h, (int64_t)d, d_mrow, (int)BK, (int)d, states, stream), "gather markers");
     RECORD(record_dense("marker_states", states, {B, K, d}));
     {
@@ -1062,6 +1149,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
                 P("act_head.0.bias"), nullptr));
     RECORD(gemm(d_act, nact, act_hid, 256, P("act_head.2.weight"), B, nact, 256, RAYA_EPI_NONE, P("act_head.2.bias"),
                 nullptr));
+    SPAN_END(sp_stage);
     RECORD(record_dense("act_logits", d_act, {B, nact}));
 
     const std::pair<float *, const float *> outs[] = {{out->logits, d_logits},
@@ -1075,6 +1163,13 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
             TRY_HIP(hipMemcpyAsync(outs[i].first, outs[i].second, sizes[i] * 4, hipMemcpyDeviceToHost, stream),
                     "download outputs");
     TRY_HIP(hipStreamSynchronize(stream), "forward");
+    for (const auto &sp : spans.v) {
+        float ms = 0.f;
+        TRY_HIP(hipEventElapsedTime(&ms, sp.e0, sp.e1), "stage time");
+        m.stages.emplace_back(sp.name, (double)ms);
+    }
+#undef SPAN
+#undef SPAN_END
 #undef RECORD
     return ok();
 }

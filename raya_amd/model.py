@@ -128,6 +128,19 @@ class Model:
         _check(C.lib().raya_model_get_info(self._h, ctypes.byref(i)))
         return {name: getattr(i, name) for name, _ in C.ModelInfoC._fields_}
 
+    def set_profiling(self, level: int) -> None:
+        """0: off; 1: an event pair around every stage (embedding, each layer, final norm,
+        head layers, scorer + act head); 2: also around every kernel of an encoder layer."""
+        _check(C.lib().raya_model_set_profiling(self._h, int(level)))
+
+    def stage_times(self) -> list[tuple[str, float]]:
+        """(name, milliseconds) of every span the last forward recorded, in order."""
+        n = ctypes.c_uint64()
+        _check(C.lib().raya_model_stage_times(self._h, None, 0, ctypes.byref(n)))
+        buf = (C.StageTimeC * max(1, n.value))()
+        _check(C.lib().raya_model_stage_times(self._h, buf, n.value, ctypes.byref(n)))
+        return [(buf[i].name.decode(), buf[i].ms) for i in range(n.value)]
+
     def forward(self, inp: ForwardInput, trace: Trace | None = None,
                 local_mask: Mask | None = None) -> ForwardOutput:
         """Network::forward on one sequence (the trace has the reference's [1, seq, …] shapes)."""

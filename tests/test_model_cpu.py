@@ -254,3 +254,14 @@ def test_synthetic_checkpoint_round_trips(tmp_path):
     info = M.Model.load(str(tmp_path)).info
     assert (info["hidden_size"], info["num_hidden_layers"], info["n_act"]) == (128, 2, 2)
     assert info["norm_eps"] == 1e-12 and info["head_layers"] == 0
+
+
+def test_profiling_level_is_checked_and_starts_empty():
+    m = load64()
+    assert m.stage_times() == []
+    for level in (0, 1, 2):
+        m.set_profiling(level)
+        assert m.stage_times() == []
+    for bad in (-1, 3):
+        with pytest.raises(M.InputError, match="profiling level"):
+            m.set_profiling(bad)

@@ -184,3 +184,41 @@ def test_half_precision_weights_are_widened_exactly(tmp_path):
     a = M.Model.load(cdir16).forward_batch(*batch)
     b = M.Model.load(cdir32).forward_batch(*batch)
     assert np.array_equal(a.act_logits, b.act_logits) and np.array_equal(a.pooled, b.pooled)
+
+
+def test_stage_timing_spans_and_outputs_unchanged():
+    """Profiling records one span per stage (level 1) and per layer kernel (level 2)
+    without changing any output."""
+    cfg, model, g, valid = load_case("medium")
+    inp = golden_input(g, valid)
+    print(f"stage timing: {cfg.layers} layers, {cfg.head_layers} head layers", flush=True)
+    base = model.forward(inp)
+    assert model.stage_times() == []
+    model.set_profiling(1)
+    out1 = model.forward(inp)
+    names1 = [n for n, _ in model.stage_times()]
+    want1 = (["embedding"] + [f"encoder_layer_{i:02d}" for i in range(cfg.layers)] + ["final_norm"]
+             + [f"head_layer_{i:02d}" for i in range(cfg.head_layers)] + ["scorer_and_act_head"])
+    assert names1 == want1
+    assert all(ms > 0.0 for _, ms in model.stage_times())
+    model.set_profiling(2)
+    out2 = model.forward(inp)
+    names2 = [n for n, _ in model.stage_times()]
+    ops = ["qkv", "attention", "attn_out", "mlp_norm", "mlp_in_geglu", "mlp_out"]
+    for i in range(cfg.layers):
+        layer = f"encoder_layer_{i:02d}"
+        subs = [n.split("/")[1] for n in names2 if n.startswith(layer + "/")]
+        assert subs == (["attn_norm"] if i > 0 else []) + ops, (layer, subs)
+    times = dict(model.stage_times())
+    for i in range(cfg.layers):
+        layer = f"encoder_layer_{i:02d}"
+        parts = sum(ms for n, ms in times.items() if n.startswith(layer + "/"))
+        assert parts <= times[layer] * 1.001 + 1e-3
+    model.set_profiling(0)
+    out0 = model.forward(inp)
+    assert model.stage_times() == []
+    for o in (out1, out2, out0):
+        for f in ("logits", "probabilities", "act_logits", "features", "pooled"):
+            assert np.array_equal(getattr(o, f), getattr(base, f)), f
+    with pytest.raises(M.InputError):
+        model.set_profiling(3)
