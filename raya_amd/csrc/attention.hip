@@ -67,7 +67,10 @@ __device__ __forceinline__ int fdiv(int n, FastDiv f) {
 struct Plan {
     int total, half_bits, n_qt;
     FastDiv by_qt, by_heads, by_arg;  // by_arg: the BlockDiag width (1 otherwise)
+    int pairs_per_xcd;                 // > 0: whole (sequence, head) pairs per XCD
 };
+
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroup i runs on XCD i mod 8
 
 // Mask::key_range (attention.rs:48-59) plus BlockDiag, clipped to valid.
 // mask_arg was clamped to seq by the host, so no sum below overflows int32
@@ -140,10 +143,28 @@ __device__ __forceinline__ Item decode(const AttnLaunch &a, const Plan &p, int i
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Bijection of [0, total) used to assign items to workgroups.  The
-// dispatcher places workgroup i on an XCD and shader engine by the low bits
-// of i, so items taken in (sequence, head, tile) order, or through any affine
-// map modulo total, would pin each tile position (and so each share of
+__device__ __forceinline__ int scatter(int i, int total, int half_bits);
+
+// The item workgroup `bid` computes.  When the number of (sequence, head)
+// pairs is a multiple of the XCD count, XCD x takes pairs x, x + 8, x + 16, ...
+// and walks each one tile by tile: the workgroups running together on an XCD
+// read neighbouring rows (DRAM pages stay open; overlapping key ranges of
+// Block3 and Sliding hit in that XCD's L2), while the heads of each sequence,
+// and with them its padding, spread over all XCDs.  Otherwise a scattered
+// order.
+__device__ __forceinline__ int item_of(int bid, const Plan &p) {
+    if (p.pairs_per_xcd > 0) {
+        const int x = bid % kXcds, j = bid / kXcds;
+        const int pj = fdiv(j, p.by_qt);
+        return (pj * kXcds + x) * p.n_qt + (j - pj * p.n_qt);
+    }
+    return scatter(bid, p.total, p.half_bits);
+}
+
+// Bijection of [0, total), the fallback assignment of items to workgroups.
+// The dispatcher places workgroup i on an XCD and shader engine by the low
+// bits of i, so items taken in (sequence, head, tile) order, or through any
+// affine map modulo total, would pin each tile position (and so each share of
 // padding) to a fixed group of CUs.  A 4-round Feistel network over 2 *
 // half_bits bits, cycle-walked back into [0, total), decorrelates them.
 __device__ __forceinline__ int scatter(int i, int total, int half_bits) {
@@ -377,7 +398,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     const float c_exp = fabsf(a.scale) * kLog2e;
     const float q_sign = a.scale < 0.f ? -1.f : 1.f;
 
-    const Item it = decode(a, p, scatter(blockIdx.x, p.total, p.half_bits));
+    const Item it = decode(a, p, item_of(blockIdx.x, p));
     // Packed sequences start at a row offset and have no padded rows in memory.
     const bool packed = a.seq_start != nullptr;
     const int64_t row0 = packed ? (int64_t)a.seq_start[it.b] : 0;
@@ -567,6 +588,8 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     p.by_qt = make_fastdiv((uint32_t)n_qt);
     p.by_heads = make_fastdiv((uint32_t)a.heads);
     p.by_arg = make_fastdiv(a.mask_kind == RAYA_MASK_BLOCKDIAG ? (uint32_t)a.mask_arg : 1u);
+    const int64_t pairs = (int64_t)a.heads * a.batch;
+    p.pairs_per_xcd = pairs % kXcds == 0 ? (int)(pairs / kXcds) : 0;
     hipLaunchKernelGGL((attend_kernel<DP, FUSED>), dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
     return hipGetLastError();
 }
