@@ -143,6 +143,27 @@ __device__ __forceinline__ Item decode(const AttnLaunch &a, const Plan &p, int i
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Cross-lane reductions over lanes i, i ^ 16 (resp. i ^ 32) without the LDS
+// crossbar: v_permlane16_swap with both operands x swaps the odd 16-lane rows
+// of one copy with the even rows of the other, so lane i of the two results
+// holds x[i] and x[i ^ 16] in some order (likewise for 32-lane halves).
+__device__ __forceinline__ float max_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ int scatter(int i, int total, int half_bits);
 
 // The item workgroup `bid` computes.  When the number of (sequence, head)
@@ -310,8 +331,7 @@ __device__ __forceinline__ void softmax_tile(floatx4 (&sacc)[4], floatx4 (&oacc)
     for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) tmax = fmaxf(tmax, sacc[t][r]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = max_xor32(max_xor16(tmax));
     const float m_new = fmaxf(m, tmax);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
     if (!first) {  // rescale what earlier tiles accumulated
@@ -540,8 +560,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         barrier_only();
         if (active) pv_tile<DP>(vs, sacc, g, li, oacc);
     }
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = sum_xor32(sum_xor16(l));
 
     // Register r of oacc[n] holds dim g DQ + NT r + n of row qi; rows at or
     // beyond valid hold zeros (every key was masked) and are stored as such.
