@@ -49,7 +49,9 @@ def test_nan_and_inf_propagate(hip_gemm):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (3, 5, 7), (17, 9, 33), (64, 64, 64), (130, 31, 257),
-                                   (256, 2304, 768), (300, 768, 3072), (129, 6144, 768)])
+                                   (256, 2304, 768), (300, 768, 3072), (129, 6144, 768),
+                                   # k = 16, 32, 48: one, two and three 16-deep slabs in the LDS ring
+                                   (70, 40, 16), (70, 40, 32), (200, 130, 48)])
 def test_within_the_reordering_bound(hip_gemm, m, n, k):
     rng = np.random.default_rng(m * 7 + n)
     a = rng.standard_normal((m, k)).astype(np.float32)
