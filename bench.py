@@ -119,6 +119,31 @@ def make_inputs(wl):
     return qkv, valid
 
 
+def host_cpu() -> dict:
+    """CPU model and core counts of this host (the baseline's context)."""
+    model, cores = "unknown", set()
+    try:
+        phys = core = None
+        for line in open("/proc/cpuinfo"):
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "model name" and model == "unknown":
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif not key and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus_usable": len(os.sched_getaffinity(0)),
+            "logical_cpus": os.cpu_count(), "physical_cores": len(cores) or None}
+
+
 def cpu_baseline(qkv, valid, wl, budget_s: float):
     """The reference's Tiled algorithm (AVX2+FMA when present) on this host's cores."""
     import oracle
@@ -159,6 +184,7 @@ def cpu_baseline(qkv, valid, wl, budget_s: float):
                    f"median of {len(times)} runs ({med * 1e3:.1f} ms each)"),
         "t1_value": f1 / t1 / 1e12,
         "t1_sample": f"first {n1} sequences, 1 thread, {t1 * 1e3:.1f} ms",
+        "host": host_cpu(),
     }
 
 
@@ -339,6 +365,7 @@ def encoder_cpu_baseline(ckpt, ids, valid, pos, mask, qtype, gpu_out, budget_s: 
             break
     dt = time.perf_counter() - t0
     return {"value": done / dt, "unit": "sequences/s", "cores": threads, "kind": "port",
+            "host": host_cpu(),
             "sample": (f"first {done} sequences of the batch ({int(valid[:done].sum())} tokens), "
                        f"one at a time, {dt:.1f} s"),
             "gpu_vs_cpu_act_logits_max_abs": diff}
