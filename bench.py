@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of raya's block-local attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload NAME] [--no-encoder]
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--workload NAME] [--no-encoder]
 
 A step is one launch of the fused fp32 attention kernel over one whole batch
 whose Q, K, V (seeded N(0, 1)) are already resident in HBM.  The default
@@ -374,7 +374,7 @@ def encoder_cpu_baseline(ckpt, ids, valid, pos, mask, qtype, gpu_out, budget_s: 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default=DEFAULT, choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
