@@ -121,3 +121,48 @@ def test_default_params():
     p = R.AttnParams.new(R.Mask.BLOCK3, 10, 40)
     assert p.block == 128 and p.valid_len == 10
     assert np.float32(p.scale) == np.float32(1.0) / np.sqrt(np.float32(40))
+
+
+C_CLIENT = r"""
+#include "raya_hip.h"
+#include <stdio.h>
+#include <string.h>
+
+int main(void) {
+    /* Shape errors come back as codes with the reference's text, before any GPU work. */
+    raya_attn_shape shape = {0, 16, 8};
+    raya_attn_params params;
+    float buf[1] = {0.0f};
+    int rc;
+    memset(&params, 0, sizeof params);
+    params.mask_kind = RAYA_MASK_FULL;
+    params.scale = 1.0f;
+    params.block = 128;
+    rc = raya_attend(&shape, &params, buf, 0, buf, 0, buf, 0, buf, 0);
+    printf("%s|%s|%d|%d|%s\n", raya_attention_name(), raya_gemm_name(), rc, raya_last_error()->code,
+           raya_last_error()->message);
+    return 0;
+}
+"""
+
+
+def test_header_builds_a_plain_c_client(tmp_path):
+    """include/raya_hip.h compiles as C99 and a C program links against libraya_hip.so
+    (what a cgo / bindgen / build.rs consumer does)."""
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    src = tmp_path / "client.c"
+    src.write_text(C_CLIENT)
+    exe = tmp_path / "client"
+    libdir = os.path.dirname(C.LIB_PATH)
+    subprocess.run([gcc, "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src),
+                    "-L", libdir, "-lraya_hip", f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.strip()
+    name, gemm, rc, code, msg = out.split("|", 4)
+    assert (name, gemm) == ("hip-gfx950", "hip-gfx950-mfma")
+    assert int(rc) == int(code) == C.RAYA_ERR_SHAPE
+    assert msg.startswith("invalid shape")
