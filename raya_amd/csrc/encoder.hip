@@ -58,6 +58,62 @@ __global__ void __launch_bounds__(64 * kRowsPerBlock)
     }
 }
 
+// The same LayerNorm for rows of NC * 256 floats (16-byte aligned rows): each lane
+// holds NC float4 of the row in registers, so the row is read once.
+template <int NC>
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+    layer_norm_vec_kernel(const float *x, int64_t ldx, const int32_t *gather, const float *w,
+                          const float *b, float eps, int rows, float *out, int64_t ldo,
+                          const float *add, const int32_t *row_seq, const int32_t *seq_index,
+                          float *out_add) {
+    constexpr int d = NC * 256;
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int64_t src = gather ? (int64_t)gather[row] : (int64_t)row;
+    const float *xr = x + src * ldx;
+    float4 v[NC];
+#pragma unroll
+    for (int i = 0; i < NC; ++i) v[i] = *(const float4 *)(xr + 256 * i + 4 * lane);
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) s += ((double)v[i].x + (double)v[i].y) + ((double)v[i].z + (double)v[i].w);
+    const double mean = wave_sum(s) / (double)d;
+    double q = 0.0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const double a = (double)v[i].x - mean, bb = (double)v[i].y - mean;
+        const double c = (double)v[i].z - mean, e = (double)v[i].w - mean;
+        q += (a * a + bb * bb) + (c * c + e * e);
+    }
+    const double var = wave_sum(q) / (double)d;
+    const double inv = 1.0 / sqrt(var + (double)eps);
+    const float *addr = add ? add + (int64_t)seq_index[row_seq[row]] * d : nullptr;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+        const int c = 256 * i + 4 * lane;
+        const float4 wv = *(const float4 *)(w + c);
+        float4 y;
+        y.x = __fmul_rn((float)(((double)v[i].x - mean) * inv), wv.x);
+        y.y = __fmul_rn((float)(((double)v[i].y - mean) * inv), wv.y);
+        y.z = __fmul_rn((float)(((double)v[i].z - mean) * inv), wv.z);
+        y.w = __fmul_rn((float)(((double)v[i].w - mean) * inv), wv.w);
+        if (b) {
+            const float4 bv = *(const float4 *)(b + c);
+            y.x = __fadd_rn(y.x, bv.x);
+            y.y = __fadd_rn(y.y, bv.y);
+            y.z = __fadd_rn(y.z, bv.z);
+            y.w = __fadd_rn(y.w, bv.w);
+        }
+        if (out) *(float4 *)(out + (int64_t)row * ldo + c) = y;
+        if (out_add) {
+            const float4 av = *(const float4 *)(addr + c);
+            *(float4 *)(out_add + (int64_t)row * ldo + c) =
+                make_float4(__fadd_rn(y.x, av.x), __fadd_rn(y.y, av.y), __fadd_rn(y.z, av.z), __fadd_rn(y.w, av.w));
+        }
+    }
+}
+
 // ops::rope_in_place (ops.rs:118-141) on the q and k sections of a packed
 // [rows][3 d] projection: for head h and i < half, (a, b) = (x[i], x[i + half])
 // becomes (a cos - b sin, b cos + a sin) at the row's position.  Each product
@@ -151,6 +207,27 @@ unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per)
 
 hipError_t launch_layer_norm(const LayerNormLaunch &l, hipStream_t stream) {
     if (l.rows == 0) return hipSuccess;
+    const auto aligned = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    const bool vec = l.d % 256 == 0 && l.d <= 1024 && l.ldx % 4 == 0 && l.ldo % 4 == 0 && aligned(l.x) &&
+                     aligned(l.w) && aligned(l.b) && aligned(l.out) && aligned(l.add) && aligned(l.out_add);
+    if (vec) {
+        const dim3 grid(blocks_for(l.rows, kRowsPerBlock)), block(64 * kRowsPerBlock);
+        switch (l.d / 256) {
+        case 1: hipLaunchKernelGGL(layer_norm_vec_kernel<1>, grid, block, 0, stream, l.x, l.ldx, l.gather, l.w,
+                                   l.b, l.eps, l.rows, l.out, l.ldo, l.add, l.row_seq, l.seq_index, l.out_add);
+                break;
+        case 2: hipLaunchKernelGGL(layer_norm_vec_kernel<2>, grid, block, 0, stream, l.x, l.ldx, l.gather, l.w,
+                                   l.b, l.eps, l.rows, l.out, l.ldo, l.add, l.row_seq, l.seq_index, l.out_add);
+                break;
+        case 3: hipLaunchKernelGGL(layer_norm_vec_kernel<3>, grid, block, 0, stream, l.x, l.ldx, l.gather, l.w,
+                                   l.b, l.eps, l.rows, l.out, l.ldo, l.add, l.row_seq, l.seq_index, l.out_add);
+                break;
+        default: hipLaunchKernelGGL(layer_norm_vec_kernel<4>, grid, block, 0, stream, l.x, l.ldx, l.gather, l.w,
+                                    l.b, l.eps, l.rows, l.out, l.ldo, l.add, l.row_seq, l.seq_index, l.out_add);
+                 break;
+        }
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(layer_norm_kernel, dim3(blocks_for(l.rows, kRowsPerBlock)),
                        dim3(64 * kRowsPerBlock), 0, stream, l.x, l.ldx, l.gather, l.w, l.b, l.eps,
                        l.rows, l.d, l.out, l.ldo, l.add, l.row_seq, l.seq_index, l.out_add);

@@ -136,8 +136,9 @@ def random_batch(rng, cfg, b, seq, k):
     return ids, valid, pos, mask, qtype
 
 
-@pytest.mark.parametrize("hidden,heads", [(128, 2), (64, 2)])
+@pytest.mark.parametrize("hidden,heads", [(128, 2), (64, 2), (256, 4)])
 def test_batch_matches_oracle_per_sequence(tmp_path, hidden, heads):
+    """hidden 256: the row-in-registers LayerNorm (rows of a multiple of 256 floats)."""
     cfg, cdir, w = make_model(tmp_path, hidden, heads)
     model = M.Model.load(cdir)
     rng = np.random.default_rng(hidden)
