@@ -48,41 +48,24 @@ __device__ __forceinline__ float activate(float x) {
     else return x;
 }
 
-#ifndef GEMM_ORDER
-#define GEMM_ORDER 2
-#endif
-#ifndef GEMM_GROUP_M
-#define GEMM_GROUP_M 8
-#endif
-constexpr int kXcds = 8;
-#ifndef GEMM_USE_RING
-#define GEMM_USE_RING 1
-#endif
-constexpr bool kUseRing = GEMM_USE_RING;  // workgroup i runs on XCD i mod 8, each with its own L2
+constexpr int kXcds = 8;     // workgroup i runs on XCD i mod 8, each with its own L2
+constexpr int kGroupM = 8;   // row blocks walked together by the tile order
 
 // Output tile of workgroup `bid`.  Each XCD takes a contiguous range of the
 // tile sequence, and the sequence walks GROUP_M row blocks at a time, column
 // by column, so a B column tile is reused GROUP_M times and the A row blocks of
 // a group stay in that XCD's L2 while all of B streams past them.
 __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int &tm, int &tn) {
-    int t = bid;
-    if (GEMM_ORDER >= 1) {
-        const int total = tiles_m * tiles_n;
-        const int per = total / kXcds, rem = total % kXcds;
-        const int xcd = bid % kXcds, slot = bid / kXcds;
-        t = xcd * per + min(xcd, rem) + slot;
-    }
-    if (GEMM_ORDER >= 2) {
-        const int width = GEMM_GROUP_M * tiles_n;
-        const int group = t / width, first = group * GEMM_GROUP_M;
-        const int size = min(tiles_m - first, GEMM_GROUP_M);
-        const int r = t - group * width;
-        tm = first + r % size;
-        tn = r / size;
-    } else {
-        tm = t / tiles_n;
-        tn = t % tiles_n;
-    }
+    const int total = tiles_m * tiles_n;
+    const int per = total / kXcds, rem = total % kXcds;
+    const int xcd = bid % kXcds, slot = bid / kXcds;
+    const int t = xcd * per + min(xcd, rem) + slot;
+    const int width = kGroupM * tiles_n;
+    const int group = t / width, first = group * kGroupM;
+    const int size = min(tiles_m - first, kGroupM);
+    const int r = t - group * width;
+    tm = first + r % size;
+    tn = r / size;
 }
 
 // Loads 4 consecutive k values of row `row` (zero outside [0, rows) x [0, k)).
@@ -379,7 +362,7 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
     } else if (g.rope_cos) {
         return hipErrorInvalidValue;
     }
-    if (ring_ok && kUseRing) {
+    if (ring_ok) {
         if (g.rope_cos)
             hipLaunchKernelGGL((gemm_ring_kernel<ACT, ACT == RAYA_EPI_NONE>), grid, block, 0, stream, g);
         else
