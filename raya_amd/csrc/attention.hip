@@ -13,8 +13,8 @@
 //
 // Computing the transposed products puts each query in one lane column
 // (lane % 16) of every accumulator, so the softmax statistics of a query live
-// in the four lanes {q, q+16, q+32, q+48}: a row maximum needs two xor
-// shuffles and the row sum is reduced once at the end.  Keys outside a row's
+// in the four lanes {q, q+16, q+32, q+48}: a row maximum needs two cross-lane
+// steps (lanes i ^ 16, i ^ 32) and the row sum is reduced once at the end.  Keys outside a row's
 // interval (mask edges, key padding) are set to -inf in registers.  Rows at or
 // beyond valid_len are written as exact zeros, as Naive::attend does
 // (crates/raya-kernels/src/naive.rs:28-31).
@@ -391,11 +391,11 @@ __device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4
 // clamped in-range address: their scores are masked, their V rows get weight
 // zero, and Q is zero on the padded dims.
 //
-// The body takes the K and V tiles as restrict pointers: inlined, that gives
-// their accesses distinct alias scopes, so the compiler knows the V tile's DMA
-// (still in flight during QK^T) does not write the K tile it reads.
-// FUSED (head_dim exactly 64): every tile's loads are issued by the asm blocks
-// above, so V stays in flight during QK^T and the softmax.
+// For head dims other than 64 the loads are compiler builtins, and the
+// compiler waits for every LDS DMA in flight before any LDS read, so a tile's V
+// has landed before its QK^T starts.  FUSED (head_dim exactly 64): every tile's
+// loads are issued by the asm blocks above with explicit waits, so V stays in
+// flight during QK^T and the softmax.
 template <int DP, bool FUSED>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs) {
