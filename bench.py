@@ -471,6 +471,17 @@ def main() -> int:
                               "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
                               "traffic": traffic}
 
+    # One launch of the instrumented kernel after the timed region: where the
+    # waves' cycles go (the reference's stage-timing split, tiled/stages.rs).
+    st = kernel.attend_batched_stages(q, k, v, out, vl, mask, stream=stream)
+    pct = st.percentages()
+    waves = st.qk + st.softmax + st.pv + st.load_wait
+    result["stage_split"] = {
+        "qk_pct": pct[0], "softmax_pct": pct[1], "pv_pct": pct[2],
+        "load_wait_of_wave_cycles_pct": 100.0 * st.load_wait / waves, "tiles": st.tiles,
+        "source": "one instrumented launch after the timed region; shares of per-wave shader "
+                  "clock cycles (qk/softmax/pv as in the reference's StageTimes::percentages)"}
+
     if not args.no_cpu_baseline:
         log("cpu baseline")
         cpu_out, cb = cpu_baseline(qkv, valid, wl, args.cpu_seconds)

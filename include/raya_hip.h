@@ -87,6 +87,29 @@ int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params,
                 const float *q, size_t q_len, const float *k, size_t k_len,
                 const float *v, size_t v_len, float *out, size_t out_len);
 
+/* Per-stage totals of the attention kernel in shader clock cycles, summed over
+ * waves: the device counterpart of StageTimes (crates/raya-kernels/src/tiled/
+ * stages.rs:3-31).  As there, only the shares are meaningful: waves of one
+ * compute unit overlap, so the sums exceed the kernel's duration. */
+typedef struct raya_stage_cycles {
+    uint64_t qk;        /* S^T = K Q^T of each tile (the reference's qk_ns) */
+    uint64_t softmax;   /* masking, running max and sum, rescale, exp (softmax_ns) */
+    uint64_t pv;        /* O^T += V^T P^T (pv_ns) */
+    uint64_t load_wait; /* K/V load issue, waits for them and the workgroup barriers
+                           (no reference counterpart: its loads are inside the stages) */
+    uint64_t tiles;     /* computed tiles of 16 query rows x 64 keys (tiles) */
+} raya_stage_cycles;
+
+/* Tiled::attend_with_stages (crates/raya-kernels/src/tiled/mod.rs:61-126) on
+ * host slices: raya_attend through an instrumented copy of the kernel that
+ * reads the shader clock around each tile's stages (raya_attend itself carries
+ * no timing code).  *stages receives this call's totals; out equals
+ * raya_attend's bit for bit. */
+int raya_attend_with_stages(const raya_attn_shape *shape, const raya_attn_params *params,
+                            const float *q, size_t q_len, const float *k, size_t k_len,
+                            const float *v, size_t v_len, float *out, size_t out_len,
+                            raya_stage_cycles *stages);
+
 /* Row strides of one operand in floats.  All zero selects the dense
  * [batch][heads][seq][head_dim] layout. */
 typedef struct raya_attn_layout {
@@ -117,6 +140,14 @@ typedef struct raya_attn_batch {
 int raya_attend_batched(const raya_attn_batch *desc, const int32_t *valid_len,
                         const float *q, const float *k, const float *v, float *out,
                         void *stream);
+
+/* raya_attend_with_stages for a device batch: raya_attend_batched through the
+ * instrumented kernel.  `stages` is a device pointer; the totals are ADDED
+ * to it (StageTimes::merge), so zero it before the first call.  Outputs equal
+ * raya_attend_batched's bit for bit.  Asynchronous on `stream`. */
+int raya_attend_batched_stages(const raya_attn_batch *desc, const int32_t *valid_len,
+                               const float *q, const float *k, const float *v, float *out,
+                               raya_stage_cycles *stages, void *stream);
 
 /* GemmBackend::matmul_nt (crates/raya-kernels/src/gemm.rs:2-11) on host
  * slices: out[m][n] = sum_t a[m][t] * b[n][t].  Length mismatches return

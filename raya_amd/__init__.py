@@ -6,8 +6,8 @@ reference's `raya-kernels` interface (see ``raya_amd.kernels``).
 """
 from .kernels import (AttentionKernel, AttnParams, AttnShape, BLOCK, DeviceError, GemmBackend,
                       HipAttention, HipGemm, KernelError, LengthError, Mask, ShapeError,
-                      UnsupportedError, WINDOW)
+                      StageTimes, UnsupportedError, WINDOW)
 
 __all__ = ["AttentionKernel", "AttnParams", "AttnShape", "BLOCK", "DeviceError", "GemmBackend",
            "HipAttention", "HipGemm", "KernelError", "LengthError", "Mask", "ShapeError",
-           "UnsupportedError", "WINDOW"]
+           "StageTimes", "UnsupportedError", "WINDOW"]

@@ -78,6 +78,10 @@ class ForwardOutputC(ctypes.Structure):
                 ("logits", "probabilities", "act_logits", "features", "pooled")]
 
 
+class StageCyclesC(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in ("qk", "softmax", "pv", "load_wait", "tiles")]
+
+
 class StageTimeC(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 48), ("ms", ctypes.c_double)]
 
@@ -98,7 +102,12 @@ SIGNATURES = [
     ("raya_gemm_name", ctypes.c_char_p, []),
     ("raya_attend", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
                                    _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
+    ("raya_attend_with_stages", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
+                                               _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz,
+                                               ctypes.POINTER(StageCyclesC)]),
     ("raya_attend_batched", ctypes.c_int, [ctypes.POINTER(AttnBatchC), _vp, _vp, _vp, _vp, _vp, _vp]),
+    ("raya_attend_batched_stages", ctypes.c_int, [ctypes.POINTER(AttnBatchC), _vp, _vp, _vp, _vp, _vp,
+                                                  _vp, _vp]),
     ("raya_matmul_nt", ctypes.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _u64, _u64, _u64]),
     ("raya_matmul_nt_device", ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _u64, _u64, _u64,
                                              ctypes.POINTER(GemmEpilogueC), _vp]),

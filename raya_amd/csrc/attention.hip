@@ -384,6 +384,42 @@ __device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4
     }
 }
 
+// Stage clock of the instrumented kernel (raya_attend_batched_stages): the
+// shader clock (s_memtime) is read at each stage boundary of a tile and the
+// difference added to that stage's total.  The scheduling barriers keep the
+// compiler from moving work across a read; settle() makes the read wait until
+// a stage's last result exists (a VALU op consumes it, so an MFMA result must
+// have been written, and the asm keeps that op before the read).
+struct StageClock {
+    uint64_t last, qk, softmax, pv, load_wait;
+    uint32_t tiles;
+};
+
+__device__ __forceinline__ uint64_t clock_now() {
+    __builtin_amdgcn_sched_barrier(0);
+    const uint64_t t = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_sched_barrier(0);
+    return t;
+}
+
+__device__ __forceinline__ void settle(float x) {
+    const int s = __builtin_amdgcn_readfirstlane(__float_as_int(x));
+    asm volatile("" ::"s"(s));
+}
+
+// Every accumulator chain of a stage (the MFMAs of different chains overlap).
+template <int N>
+__device__ __forceinline__ void settle(const floatx4 (&x)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) settle(x[i][3]);
+}
+
+__device__ __forceinline__ void lap(StageClock *c, uint64_t &bucket) {
+    const uint64_t t = clock_now();
+    bucket += t - c->last;
+    c->last = t;
+}
+
 // One workgroup computes one item.  Q goes straight to registers; each K/V
 // tile goes straight from HBM to LDS (global_load_lds_dwordx4, no staging
 // registers), so the kernel runs at high occupancy and other workgroups hide
@@ -396,9 +432,9 @@ __device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4
 // has landed before its QK^T starts.  FUSED (head_dim exactly 64): every tile's
 // loads are issued by the asm blocks above with explicit waits, so V stays in
 // flight during QK^T and the softmax.
-template <int DP, bool FUSED>  // head_dim padded to a multiple of 16
+template <int DP, bool FUSED, bool TIMED>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
-                                            float *__restrict__ vs) {
+                                            float *__restrict__ vs, StageClock *clk) {
     static_assert(!FUSED || DP == 64, "the fused issue is written for head_dim 64");
     constexpr int DQ = DP / 4;   // head-dim slice owned by one lane group
     constexpr int NT = DP / 16;  // 16-dim output tiles
@@ -521,6 +557,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // the PV operand of (t, r) is row 16t + 4r + g, dims NT li .. NT li + NT.
     const int k_row0 = 4 * (li & 3) + (li >> 2);
 
+    if constexpr (TIMED) clk->last = clock_now();
     for (int kt = it.k_lo; kt < it.k_hi; kt += kKeys) {
         if (kt != it.k_lo) {
             // Every wave's LDS reads of the previous tile have returned.
@@ -550,15 +587,33 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         }
         const bool active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
         floatx4 sacc[4];
+        if constexpr (TIMED) lap(clk, clk->load_wait);
         if (active) {
             qk_tile<DP>(ks, qreg, g, k_row0, sacc);
+            if constexpr (TIMED) {
+                settle(sacc);
+                lap(clk, clk->qk);
+                ++clk->tiles;
+            }
             softmax_tile<NT>(sacc, oacc, m, l, kt == it.k_lo,
                              !(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi), rr.lo - kt - g,
                              rr.hi - kt - g, c_exp);
+            if constexpr (TIMED) {
+                settle(l);
+                settle(oacc);
+                lap(clk, clk->softmax);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's V loads have landed
         barrier_only();
-        if (active) pv_tile<DP>(vs, sacc, g, li, oacc);
+        if constexpr (TIMED) lap(clk, clk->load_wait);
+        if (active) {
+            pv_tile<DP>(vs, sacc, g, li, oacc);
+            if constexpr (TIMED) {
+                settle(oacc);
+                lap(clk, clk->pv);
+            }
+        }
     }
     l = sum_xor32(sum_xor16(l));
 
@@ -585,7 +640,34 @@ template <int DP, bool FUSED>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, FUSED>(a, p, ks, vs);
+    attend_body<DP, FUSED, false>(a, p, ks, vs, nullptr);
+}
+
+// The same kernel with the stage clock.  Per-wave totals are summed in LDS,
+// then one thread per stage adds the workgroup's sum to the caller's totals.
+// An item whose rows are all padding returns from the body in every wave with
+// zero totals.
+template <int DP, bool FUSED>
+__global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_timed_kernel(const AttnLaunch a, const Plan p) {
+    __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
+    __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
+    __shared__ uint64_t part[kWaves][5];
+    StageClock c{};
+    attend_body<DP, FUSED, true>(a, p, ks, vs, &c);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        part[wave][0] = c.qk;
+        part[wave][1] = c.softmax;
+        part[wave][2] = c.pv;
+        part[wave][3] = c.load_wait;
+        part[wave][4] = c.tiles;
+    }
+    __syncthreads();
+    if (threadIdx.x < 5) {
+        uint64_t sum = 0;
+        for (int w = 0; w < kWaves; ++w) sum += part[w][threadIdx.x];
+        if (sum) atomicAdd((unsigned long long *)&a.stage_cycles->qk + threadIdx.x, (unsigned long long)sum);
+    }
 }
 
 // Half the bit width of the scatter domain: the smallest h with 4^h >= total.
@@ -609,7 +691,10 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     p.by_arg = make_fastdiv(a.mask_kind == RAYA_MASK_BLOCKDIAG ? (uint32_t)a.mask_arg : 1u);
     const int64_t pairs = (int64_t)a.heads * a.batch;
     p.pairs_per_xcd = pairs % kXcds == 0 ? (int)(pairs / kXcds) : 0;
-    hipLaunchKernelGGL((attend_kernel<DP, FUSED>), dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
+    if (a.stage_cycles)
+        hipLaunchKernelGGL((attend_timed_kernel<DP, FUSED>), dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
+    else
+        hipLaunchKernelGGL((attend_kernel<DP, FUSED>), dim3((unsigned)total), dim3(kThreads), 0, stream, a, p);
     return hipGetLastError();
 }
 

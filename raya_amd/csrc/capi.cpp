@@ -127,17 +127,11 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 using namespace raya;
 
-extern "C" {
-
-const raya_error *raya_last_error(void) { return &g_err; }
-
-const char *raya_attention_name(void) { return "hip-gfx950"; }
-
-const char *raya_gemm_name(void) { return "hip-gfx950-mfma"; }
-
-int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
-                size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
-                float *out, size_t out_len) {
+// raya_attend, and with `stages` (host) set raya_attend_with_stages: the
+// device totals live in a 256-byte slot after the four operand slots.
+static int attend_host(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
+                       size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
+                       float *out, size_t out_len, raya_stage_cycles *stages) {
     if (!shape || !params) return fail(RAYA_ERR_SHAPE, "invalid shape: null shape or params");
     int rc = check_attn(shape->heads, shape->seq, shape->head_dim, params->mask_kind,
                         params->mask_arg, params->block, &params->valid_len);
@@ -149,6 +143,7 @@ int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, co
     } bufs[4] = {{"q", q_len}, {"k", k_len}, {"v", v_len}, {"out", out_len}};
     for (const auto &bf : bufs)
         if (bf.len != numel) return fail_length(bf.name, bf.len, numel);
+    if (stages) *stages = raya_stage_cycles{};
     if (numel == 0) return ok();
     if (!q || !k || !v || !out) return fail(RAYA_ERR_SHAPE, "invalid shape: null buffer");
 
@@ -157,7 +152,7 @@ int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, co
     hipStream_t stream = nullptr;
     const size_t bytes = numel * sizeof(float);
     const size_t slot = (bytes + 255) / 256 * 256;
-    rc = workspace(4 * slot, &base, &stream);
+    rc = workspace(4 * slot + (stages ? 256 : 0), &base, &stream);
     if (rc) return rc;
     char *p = (char *)base;
     float *dq = (float *)p, *dk = (float *)(p + slot), *dv = (float *)(p + 2 * slot),
@@ -186,15 +181,47 @@ int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, co
     a.mask_kind = params->mask_kind;
     a.mask_arg = clamp_arg(params->mask_kind, params->mask_arg, shape->seq);
     a.scale = params->scale;
+    if (stages) {
+        a.stage_cycles = (raya_stage_cycles *)(p + 4 * slot);
+        if ((e = hipMemsetAsync(a.stage_cycles, 0, sizeof(raya_stage_cycles), stream)) != hipSuccess)
+            return fail_device(e, "hipMemsetAsync");
+    }
     if ((e = launch_attention(a, stream)) != hipSuccess) return fail_device(e, "attention launch");
     if ((e = hipMemcpyAsync(out, dout, bytes, hipMemcpyDeviceToHost, stream)) != hipSuccess)
+        return fail_device(e, "hipMemcpy device to host");
+    if (stages && (e = hipMemcpyAsync(stages, a.stage_cycles, sizeof(raya_stage_cycles),
+                                      hipMemcpyDeviceToHost, stream)) != hipSuccess)
         return fail_device(e, "hipMemcpy device to host");
     if ((e = hipStreamSynchronize(stream)) != hipSuccess) return fail_device(e, "hipStreamSynchronize");
     return ok();
 }
 
-int raya_attend_batched(const raya_attn_batch *d, const int32_t *valid_len, const float *q,
-                        const float *k, const float *v, float *out, void *stream) {
+extern "C" {
+
+const raya_error *raya_last_error(void) { return &g_err; }
+
+const char *raya_attention_name(void) { return "hip-gfx950"; }
+
+const char *raya_gemm_name(void) { return "hip-gfx950-mfma"; }
+
+int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
+                size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
+                float *out, size_t out_len) {
+    return attend_host(shape, params, q, q_len, k, k_len, v, v_len, out, out_len, nullptr);
+}
+
+int raya_attend_with_stages(const raya_attn_shape *shape, const raya_attn_params *params,
+                            const float *q, size_t q_len, const float *k, size_t k_len,
+                            const float *v, size_t v_len, float *out, size_t out_len,
+                            raya_stage_cycles *stages) {
+    if (!stages) return fail(RAYA_ERR_SHAPE, "invalid shape: null stages");
+    return attend_host(shape, params, q, q_len, k, k_len, v, v_len, out, out_len, stages);
+}
+
+namespace {
+
+int attend_batched(const raya_attn_batch *d, const int32_t *valid_len, const float *q, const float *k,
+                   const float *v, float *out, raya_stage_cycles *stages, void *stream) {
     if (!d) return fail(RAYA_ERR_SHAPE, "invalid shape: null descriptor");
     int rc = check_attn(d->heads, d->seq, d->head_dim, d->mask_kind, d->mask_arg, d->block, nullptr);
     if (rc) return rc;
@@ -242,9 +269,25 @@ int raya_attend_batched(const raya_attn_batch *d, const int32_t *valid_len, cons
     a.mask_kind = d->mask_kind;
     a.mask_arg = clamp_arg(d->mask_kind, d->mask_arg, d->seq);
     a.scale = d->scale;
+    a.stage_cycles = stages;
     const hipError_t e = launch_attention(a, (hipStream_t)stream);
     if (e != hipSuccess) return fail_device(e, "attention launch");
     return ok();
+}
+
+}  // namespace
+
+int raya_attend_batched(const raya_attn_batch *d, const int32_t *valid_len, const float *q,
+                        const float *k, const float *v, float *out, void *stream) {
+    return attend_batched(d, valid_len, q, k, v, out, nullptr, stream);
+}
+
+int raya_attend_batched_stages(const raya_attn_batch *d, const int32_t *valid_len, const float *q,
+                               const float *k, const float *v, float *out, raya_stage_cycles *stages,
+                               void *stream) {
+    if (!stages || ((uintptr_t)stages & 7))
+        return fail(RAYA_ERR_SHAPE, "invalid shape: `stages` must be an 8-byte aligned device pointer");
+    return attend_batched(d, valid_len, q, k, v, out, stages, stream);
 }
 
 int raya_matmul_nt(float *out, size_t out_len, const float *a, size_t a_len, const float *b,

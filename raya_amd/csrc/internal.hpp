@@ -27,6 +27,9 @@ struct AttnLaunch {
     // each operand (batch strides unused), only its valid rows exist and rows at
     // or beyond valid_len are neither read nor written.
     const int32_t *seq_start;
+    // Non-null selects the instrumented kernel, which adds its per-stage clock
+    // totals to this device struct.
+    raya_stage_cycles *stage_cycles;
 };
 
 // Largest head_dim the fused attention kernel is instantiated for.

@@ -152,6 +152,39 @@ class AttnParams:
         return AttnParams(**d)
 
 
+@dataclass
+class StageTimes:
+    """StageTimes (crates/raya-kernels/src/tiled/stages.rs:3-31), counted in
+    shader clock cycles summed over waves rather than nanoseconds summed over
+    threads; ``load_wait`` (load issue, waits and barriers) has no reference
+    counterpart and stays out of the percentages, as the reference's stages hold
+    no separate load time."""
+
+    qk: int = 0
+    softmax: int = 0
+    pv: int = 0
+    load_wait: int = 0
+    tiles: int = 0
+
+    def merge(self, other: "StageTimes") -> None:
+        self.qk += other.qk
+        self.softmax += other.softmax
+        self.pv += other.pv
+        self.load_wait += other.load_wait
+        self.tiles += other.tiles
+
+    def percentages(self):
+        """(qk, softmax, pv) as percentages of their sum, or None if nothing was timed."""
+        total = float(self.qk + self.softmax + self.pv)
+        if total <= 0.0:
+            return None
+        return (100.0 * self.qk / total, 100.0 * self.softmax / total, 100.0 * self.pv / total)
+
+    @staticmethod
+    def _from_c(c) -> "StageTimes":
+        return StageTimes(int(c.qk), int(c.softmax), int(c.pv), int(c.load_wait), int(c.tiles))
+
+
 class AttentionKernel(abc.ABC):
     """AttentionKernel (attention.rs:113-125)."""
 
@@ -213,14 +246,33 @@ class HipAttention(AttentionKernel):
         if rc:
             _raise_last(rc)
 
+    def attend_with_stages(self, shape: AttnShape, params: AttnParams, q, k, v, out) -> StageTimes:
+        """``attend`` through the instrumented kernel, returning its stage totals
+        (Tiled::attend_with_stages, crates/raya-kernels/src/tiled/mod.rs:61-126).
+        The outputs equal ``attend``'s."""
+        (qp, ql), (kp, kl), (vp, vl), (op, ol) = (
+            _host_f32(q, "q"), _host_f32(k, "k"), _host_f32(v, "v"), _host_f32(out, "out"))
+        if not out.flags.writeable:
+            raise TypeError("`out` must be writeable")
+        s = C.AttnShapeC(shape.heads, shape.seq, shape.head_dim)
+        p = C.AttnParamsC(params.mask.kind, params.scale, params.mask.arg, params.block,
+                          params.valid_len)
+        st = C.StageCyclesC()
+        rc = C.lib().raya_attend_with_stages(ctypes.byref(s), ctypes.byref(p), qp, ql, kp, kl, vp, vl,
+                                             op, ol, ctypes.byref(st))
+        if rc:
+            _raise_last(rc)
+        return StageTimes._from_c(st)
+
     def attend_batched(self, q, k, v, out, valid_len, mask: Mask, scale: float | None = None,
-                       block: int = BLOCK, layouts=None, stream=None) -> None:
+                       block: int = BLOCK, layouts=None, stream=None, stages=None) -> None:
         """Batched device path: q/k/v/out are GPU tensors viewed as
         [batch][heads][seq][head_dim] (or with explicit ``layouts``: a dict of
         name -> (batch_stride, head_stride, row_stride) in floats, plus
         ``shape`` = (batch, heads, seq, head_dim)); valid_len is a GPU int32
         tensor [batch].  Asynchronous on ``stream`` (torch's current stream by
-        default)."""
+        default).  ``stages``, a GPU int64 tensor of 5 entries, selects the
+        instrumented kernel, which adds (qk, softmax, pv, load_wait, tiles) to it."""
         import torch
 
         if layouts is None:
@@ -244,11 +296,29 @@ class HipAttention(AttentionKernel):
         desc = C.AttnBatchC(b, h, s_, d, mask.kind, scale, mask.arg, block,
                             C.AttnLayoutC(*lay["q"]), C.AttnLayoutC(*lay["k"]),
                             C.AttnLayoutC(*lay["v"]), C.AttnLayoutC(*lay["out"]))
-        rc = C.lib().raya_attend_batched(ctypes.byref(desc), _dev_ptr(valid_len, "valid_len"),
-                                         _dev_ptr(q, "q"), _dev_ptr(k, "k"), _dev_ptr(v, "v"),
-                                         _dev_ptr(out, "out"), _stream_ptr(stream))
+        ptrs = (_dev_ptr(valid_len, "valid_len"), _dev_ptr(q, "q"), _dev_ptr(k, "k"),
+                _dev_ptr(v, "v"), _dev_ptr(out, "out"))
+        if stages is None:
+            rc = C.lib().raya_attend_batched(ctypes.byref(desc), *ptrs, _stream_ptr(stream))
+        else:
+            if stages.dtype != torch.int64 or not stages.is_cuda or stages.numel() < 5 \
+                    or not stages.is_contiguous():
+                raise ShapeError("invalid shape: stages must be a contiguous GPU int64 tensor of 5 entries")
+            rc = C.lib().raya_attend_batched_stages(ctypes.byref(desc), *ptrs, _dev_ptr(stages, "stages"),
+                                                    _stream_ptr(stream))
         if rc:
             _raise_last(rc)
+
+    def attend_batched_stages(self, q, k, v, out, valid_len, mask: Mask, scale: float | None = None,
+                              block: int = BLOCK, layouts=None, stream=None) -> StageTimes:
+        """``attend_batched`` through the instrumented kernel; waits for the
+        stream and returns the launch's stage totals."""
+        import torch
+
+        stages = torch.zeros(5, dtype=torch.int64, device=q.device)
+        self.attend_batched(q, k, v, out, valid_len, mask, scale, block, layouts, stream, stages=stages)
+        (stream if stream is not None else torch.cuda.current_stream()).synchronize()
+        return StageTimes(*(int(x) for x in stages.cpu().tolist()))
 
 
 class HipGemm(GemmBackend):
