@@ -259,9 +259,98 @@ __device__ __forceinline__ void dma16(const float *src, uint32_t lds_addr) {
 
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
+// Epilogue through LDS, for out (and residual) with row strides a multiple of 4
+// floats and 16-byte aligned bases.  Bias, activation, GeGLU and RoPE are
+// applied in the accumulator layout, as in epilogue(); each wave then writes
+// its y rows to its own LDS area and reads them back row-major, so that the
+// residual reads and the stores are float4 with 256-byte (GeGLU: 128-byte) row
+// segments: a quarter of the store instructions of the accumulator layout.
+// Staged row strides: lanes i and i + 32 of a write are 4 rows apart, and
+// 4 * stride = 32 (mod 64) puts them on disjoint banks.
+constexpr int kStageStride = 72;      // 64 columns per wave
+constexpr int kStageStrideGlu = 40;   // 32 GeGLU output columns per wave
+constexpr int kStageFloats = 32 * kStageStride;  // per wave: 32 rows at a time
+
+template <int ACT, bool ROPE>
+__device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, const floatx16 (&acc)[2][2], int m0, int n0,
+                                                int wm, int wn, int li, int h, int lane, float *stg) {
+    constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
+    constexpr int COLS = GEGLU ? 32 : 64;  // output columns of this wave
+    constexpr int S = GEGLU ? kStageStrideGlu : kStageStride;
+    constexpr int C4 = COLS / 4;           // float4 per staged row
+    const int c0 = n0 + (GEGLU ? (wn >> 1) : wn);  // first output column of this wave
+    float bias[2] = {0.f, 0.f};
+    if (g.bias) {
+        if constexpr (GEGLU) {
+            const int col = min(c0 + li, g.n - 1);
+            bias[0] = g.bias[col];
+            bias[1] = g.bias[g.n + col];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bias[j] = g.bias[min(c0 + 32 * j + li, g.n - 1)];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int rr = 8 * (r >> 2) + 4 * h + (r & 3);
+            // Without a bias the accumulator is used as it is (x + 0 would turn -0 into +0).
+            if constexpr (GEGLU) {
+                const float x = g.bias ? acc[i][0][r] + bias[0] : acc[i][0][r];
+                const float gate = g.bias ? acc[i][1][r] + bias[1] : acc[i][1][r];
+                stg[rr * S + li] = gelu_erf(x) * gate;
+            } else {
+                float y[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) y[j] = activate<ACT>(g.bias ? acc[i][j][r] + bias[j] : acc[i][j][r]);
+                if constexpr (ROPE) {
+                    // Columns c and c + 32 of one 64-wide head sit in the same lane
+                    // and register of acc[i][0] and acc[i][1].
+                    const int row = min(m0 + wm + 32 * i + rr, g.m - 1);
+                    if (c0 + li < g.rope_cols) {
+                        const int64_t t = (int64_t)g.positions[row] * (kRopeHeadDim / 2) + li;
+                        const float c = g.rope_cos[t], sn = g.rope_sin[t];
+                        const float x0 = y[0], x1 = y[1];
+                        y[0] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+                        y[1] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, sn));
+                    }
+                }
+                stg[rr * S + li] = y[0];
+                stg[rr * S + 32 + li] = y[1];
+            }
+        }
+        // LDS accesses of one wave complete in order: the reads below see the
+        // writes above, and the next half's writes follow these reads.
+#pragma unroll
+        for (int t = 0; t < 32 * C4 / 64; ++t) {
+            const int idx = t * 64 + lane, rr = idx / C4, c4 = idx % C4;
+            const int row = m0 + wm + 32 * i + rr, col = c0 + 4 * c4;
+            if (row >= g.m || col >= g.n) continue;
+            float4 v = *(const float4 *)&stg[rr * S + 4 * c4];
+            float *o = g.out + (int64_t)row * g.ldo + col;
+            const float *res = g.residual ? g.residual + (int64_t)row * g.ldr + col : nullptr;
+            if (col + 4 <= g.n) {
+                if (res) {
+                    const float4 x = *(const float4 *)res;
+                    v.x += x.x;
+                    v.y += x.y;
+                    v.z += x.z;
+                    v.w += x.w;
+                }
+                *(float4 *)o = v;
+            } else {
+                const float e[4] = {v.x, v.y, v.z, v.w};
+                for (int q = 0; q < 4 && col + q < g.n; ++q) o[q] = res ? e[q] + res[q] : e[q];
+            }
+        }
+    }
+}
+
 template <int ACT, bool ROPE>
 __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch g) {
     __shared__ __attribute__((aligned(16))) float ring[RSTAGES * 2 * kTileFloats];  // 48 KB
+    static_assert(4 * kStageFloats <= RSTAGES * 2 * kTileFloats, "epilogue staging fits the ring");
 
     constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
     constexpr int OUT_BN = GEGLU ? BN / 2 : BN;
@@ -352,7 +441,14 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
         __builtin_amdgcn_s_setprio(0);
         stage = stage == RSTAGES - 1 ? 0 : stage + 1;
     }
-    epilogue<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h);
+    const bool vec_out = (g.ldo & 3) == 0 && ((uintptr_t)g.out & 15) == 0 &&
+                         (!g.residual || ((g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15) == 0));
+    if (vec_out) {
+        __syncthreads();  // every wave's reads of the last slab are done: the ring is free
+        epilogue_staged<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h, lane, ring + wave * kStageFloats);
+    } else {
+        epilogue<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h);
+    }
 }
 
 template <int ACT>

@@ -115,3 +115,37 @@ def test_device_epilogues(hip_gemm, act, residual, k):
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert np.abs(got - want).max() < 1e-4 * max(1.0, float(np.abs(want).max()))
+
+
+@pytest.mark.parametrize("act", ["none", "gelu", "geglu"])
+@pytest.mark.parametrize("residual", [False, True])
+def test_strided_out_vector_and_scalar_epilogues_agree(hip_gemm, act, residual):
+    """n = 70 inside rows of 72 floats takes the float4 (LDS-staged) epilogue, with a
+    partial last float4; rows of 70 floats take the per-element one.  Both give the
+    same bits, and the two columns past n are left alone."""
+    rng = np.random.default_rng(13)
+    m, n, k = 150, 70, 64
+    code = {"none": C.RAYA_EPI_NONE, "gelu": C.RAYA_EPI_GELU, "geglu": C.RAYA_EPI_GEGLU}[act]
+    rows_b = 2 * n if act == "geglu" else n
+    a = _dev(rng.standard_normal((m, k)).astype(np.float32))
+    b = _dev((0.1 * rng.standard_normal((rows_b, k))).astype(np.float32))
+    bias = _dev(rng.standard_normal(rows_b).astype(np.float32))
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    outs = []
+    for ld in (72, 70):
+        buf = torch.full((m, ld), 9.0, device="cuda")
+        out = buf[:, :n]
+        if residual:
+            out.copy_(_dev(res))
+        hip_gemm.matmul_nt_device(out, a, b, bias=bias, activation=code,
+                                  residual=out if residual else None)
+        torch.cuda.synchronize()
+        outs.append(buf.cpu().numpy())
+    assert np.array_equal(outs[0][:, :n], outs[1])
+    assert (outs[0][:, n:] == 9.0).all()
+    y = oracle.matmul_nt(a.cpu().numpy(), b.cpu().numpy()) + bias.cpu().numpy()
+    want = {"none": lambda: y, "gelu": lambda: oracle.gelu_array(y),
+            "geglu": lambda: oracle.gelu_array(y[:, :n]) * y[:, n:]}[act]()
+    if residual:
+        want = want + res
+    assert np.abs(outs[1] - want).max() < 1e-4 * max(1.0, float(np.abs(want).max()))
