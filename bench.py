@@ -121,27 +121,9 @@ def make_inputs(wl):
 
 def host_cpu() -> dict:
     """CPU model and core counts of this host (the baseline's context)."""
-    model, cores = "unknown", set()
-    try:
-        phys = core = None
-        for line in open("/proc/cpuinfo"):
-            key, _, val = line.partition(":")
-            key, val = key.strip(), val.strip()
-            if key == "model name" and model == "unknown":
-                model = val
-            elif key == "physical id":
-                phys = val
-            elif key == "core id":
-                core = val
-            elif not key and phys is not None and core is not None:
-                cores.add((phys, core))
-                phys = core = None
-        if phys is not None and core is not None:
-            cores.add((phys, core))
-    except OSError:
-        pass
-    return {"model": model, "logical_cpus_usable": len(os.sched_getaffinity(0)),
-            "logical_cpus": os.cpu_count(), "physical_cores": len(cores) or None}
+    from raya_amd import meta
+
+    return meta.host_cpu()
 
 
 def cpu_baseline(qkv, valid, wl, budget_s: float):
@@ -481,6 +463,13 @@ def main() -> int:
         "load_wait_of_wave_cycles_pct": 100.0 * st.load_wait / waves, "tiles": st.tiles,
         "source": "one instrumented launch after the timed region; shares of per-wave shader "
                   "clock cycles (qk/softmax/pv as in the reference's StageTimes::percentages)"}
+
+    # BenchMetadata (crates/raya-kernels/src/meta.rs): host, GPU and build; threads is
+    # the CPU baseline's worker count.
+    from raya_amd import meta
+
+    result["meta"] = meta.collect(threads=0 if args.no_cpu_baseline
+                                  else min(16, len(os.sched_getaffinity(0))))
 
     if not args.no_cpu_baseline:
         log("cpu baseline")

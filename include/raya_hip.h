@@ -78,6 +78,12 @@ const raya_error *raya_last_error(void);
 const char *raya_attention_name(void);
 const char *raya_gemm_name(void);
 
+/* How this library was built, fixed at build time as the reference's
+ * BenchMetadata fields rustc and git_commit are (crates/raya-kernels/src/
+ * meta.rs:12-27, build.rs): lines "arch=...", "compiler=...", "commit=..."
+ * and "flags=...", "unknown" where the build could not tell. */
+const char *raya_build_info(void);
+
 /* AttentionKernel::attend (crates/raya-kernels/src/attention.rs:113-125) on
  * host slices: validates like validate() (attention.rs:128-170) plus the
  * HIP kernel's limits (head_dim <= 128), copies q/k/v to the current device,

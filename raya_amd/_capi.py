@@ -100,6 +100,7 @@ SIGNATURES = [
     ("raya_last_error", ctypes.POINTER(ErrorC), []),
     ("raya_attention_name", ctypes.c_char_p, []),
     ("raya_gemm_name", ctypes.c_char_p, []),
+    ("raya_build_info", ctypes.c_char_p, []),
     ("raya_attend", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
                                    _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
     ("raya_attend_with_stages", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),

@@ -41,9 +41,35 @@ def _flags() -> list[str]:
     ]
 
 
+def _run(cmd: list[str]) -> str:
+    """First line of a command's output, or "unknown" (as build.rs's run() does)."""
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, cwd=ROOT, timeout=60)
+    except (OSError, subprocess.SubprocessError):
+        return "unknown"
+    out = r.stdout.strip()
+    return out.splitlines()[0] if r.returncode == 0 and out else "unknown"
+
+
+def _c_string(x: str) -> str:
+    return '"' + x.replace("\\", "\\\\").replace('"', '\\"') + '"'
+
+
+def _stamp() -> list[str]:
+    """What raya_build_info() reports, fixed at build time like the reference's
+    RAYA_RUSTC_VERSION and RAYA_GIT_COMMIT (crates/raya-kernels/build.rs)."""
+    flags = " ".join(f for f in _flags() if not f.startswith("-I") and not f.startswith(ROOT)
+                     and f != "-I")
+    return [f"-DRAYA_BUILD_COMPILER={_c_string(_run([hipcc(), '--version']))}",
+            f"-DRAYA_BUILD_COMMIT={_c_string(_run(['git', 'rev-parse', 'HEAD']))}",
+            f"-DRAYA_BUILD_FLAGS={_c_string(flags)}"]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     cmd = [hipcc(), *_flags(), "-c", os.path.join(CSRC, src), "-o", obj]
+    if src == "capi.cpp":
+        cmd[1:1] = _stamp()
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

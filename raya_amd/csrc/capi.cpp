@@ -204,6 +204,20 @@ const char *raya_attention_name(void) { return "hip-gfx950"; }
 
 const char *raya_gemm_name(void) { return "hip-gfx950-mfma"; }
 
+#ifndef RAYA_BUILD_COMPILER
+#define RAYA_BUILD_COMPILER "unknown"
+#endif
+#ifndef RAYA_BUILD_COMMIT
+#define RAYA_BUILD_COMMIT "unknown"
+#endif
+#ifndef RAYA_BUILD_FLAGS
+#define RAYA_BUILD_FLAGS "unknown"
+#endif
+
+const char *raya_build_info(void) {
+    return "arch=gfx950\ncompiler=" RAYA_BUILD_COMPILER "\ncommit=" RAYA_BUILD_COMMIT "\nflags=" RAYA_BUILD_FLAGS;
+}
+
 int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
                 size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
                 float *out, size_t out_len) {
