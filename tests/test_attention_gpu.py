@@ -303,3 +303,37 @@ def test_full_size_properties_b32_l2048(hip_attention):
     torch.cuda.synchronize()
     assert float((o12 - o1 - o2).abs().max()) < 2e-5
     assert bool(torch.all(torch.where(rows, True, o12 == 0)))
+
+
+def test_random_sweep_against_the_oracle(hip_attention):
+    """48 random batched launches against the oracle: batch 1-4, heads 1-3, seq 1-700,
+    every head_dim multiple of 8 up to 128, every mask with random widths (BlockDiag(b) and
+    Sliding(w) from 1 to past seq), valid lengths anywhere in [0, seq] (out-of-range values
+    are clamped by the entry point), and negative or enlarged scales."""
+    rng = np.random.default_rng(2024)
+    kinds = ["block3", "window64", "full", "sliding", "block_diag"]
+    for case in range(48):
+        b, h = int(rng.integers(1, 5)), int(rng.integers(1, 4))
+        s, d = int(rng.integers(1, 701)), 8 * int(rng.integers(1, 17))
+        kind = kinds[case % len(kinds)]
+        arg = int(rng.integers(1, s + 80))
+        if kind == "sliding":
+            mask, okind, block, window = R.Mask.sliding(arg), oracle.MASK_SLIDING, 128, arg
+        elif kind == "block_diag":
+            mask, okind, block, window = R.Mask.block_diag(arg), oracle.MASK_BLOCKDIAG, arg, 0
+        else:
+            mask, okind, block, window = MASKS[kind]
+        valid = rng.integers(-3, s + 4, size=b).astype(np.int32)
+        clamped = np.clip(valid, 0, s).astype(np.int32)
+        scale = R.kernels.default_scale(d) * float(rng.choice([1.0, -1.0, 2.0]))
+        q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+        print(f"case {case}: b{b} h{h} s{s} d{d} {kind}({arg}) valid {valid.tolist()} "
+              f"scale {scale:.4f}", flush=True)
+        want = oracle.naive_attend_batched(q, k, v, okind, clamped, scale, block=block, window=window)
+        out = torch.full((b, h, s, d), float("nan"), device="cuda")
+        hip_attention.attend_batched(_dev(q), _dev(k), _dev(v), out, _dev(valid), mask, scale=scale)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        check_close(got, want, f"case {case}")
+        for i in range(b):
+            assert (got[i, :, clamped[i]:, :] == 0).all()
