@@ -149,3 +149,55 @@ def test_strided_out_vector_and_scalar_epilogues_agree(hip_gemm, act, residual):
     if residual:
         want = want + res
     assert np.abs(outs[1] - want).max() < 1e-4 * max(1.0, float(np.abs(want).max()))
+
+
+def test_random_sweep_of_shapes_and_epilogues(hip_gemm):
+    """40 random device GEMMs against the oracle's Reference::matmul_nt: m, n, k from 1 to
+    several hundred (k a multiple of 16 in half of them, the LDS-ring kernel), every
+    activation, optional bias and residual, and row strides larger than n in a third of them.
+    The bound is the reordering bound above, carried through the epilogue (GELU's slope is
+    at most 1.13; GeGLU's product takes each factor's error times the other factor)."""
+    rng = np.random.default_rng(77)
+    acts = ["none", "gelu", "relu", "geglu"]
+    for case in range(40):
+        m, n = int(rng.integers(1, 600)), int(rng.integers(1, 400))
+        k = 16 * int(rng.integers(1, 40)) if case % 2 == 0 else int(rng.integers(1, 400))
+        act = acts[case % 4]
+        rows_b = 2 * n if act == "geglu" else n
+        has_bias, has_res = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        ld = n + (4 * int(rng.integers(1, 4)) if case % 3 == 0 else 0)
+        print(f"case {case}: m{m} n{n} k{k} {act} bias {has_bias} residual {has_res} ld {ld}", flush=True)
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        b = (0.1 * rng.standard_normal((rows_b, k))).astype(np.float32)
+        bias = rng.standard_normal(rows_b).astype(np.float32) if has_bias else np.zeros(rows_b, np.float32)
+        res = rng.standard_normal((m, n)).astype(np.float32)
+        y = oracle.matmul_nt(a, b).astype(np.float64) + bias
+        err = bound(a, b) + 1e-7 * np.abs(y)
+        if act == "geglu":
+            x, g = y[:, :n], y[:, n:]
+            gx = oracle.gelu_array(x.astype(np.float32)).astype(np.float64)
+            want = gx * g
+            err = 1.13 * err[:, :n] * np.abs(g) + np.abs(gx) * err[:, n:] + 1e-6 * np.abs(want)
+        elif act == "gelu":
+            want = oracle.gelu_array(y.astype(np.float32)).astype(np.float64)
+            err = 1.13 * err + 1e-6 * np.abs(want)
+        elif act == "relu":
+            want = np.maximum(y, 0)
+        else:
+            want = y
+        if has_res:
+            want = want + res
+        buf = torch.full((m, ld), 9.0, device="cuda")
+        out = buf[:, :n]
+        if has_res:
+            out.copy_(_dev(res))
+        code = {"none": C.RAYA_EPI_NONE, "gelu": C.RAYA_EPI_GELU, "relu": C.RAYA_EPI_RELU,
+                "geglu": C.RAYA_EPI_GEGLU}[act]
+        hip_gemm.matmul_nt_device(out, _dev(a), _dev(b), bias=_dev(bias) if has_bias else None,
+                                  activation=code, residual=out if has_res else None)
+        torch.cuda.synchronize()
+        got = buf.cpu().numpy()
+        diff = np.abs(got[:, :n].astype(np.float64) - want)
+        tol = 2 * err + 1e-6 * (1 + np.abs(want))
+        assert (diff <= tol).all(), (case, float((diff - tol).max()))
+        assert (got[:, n:] == 9.0).all()
