@@ -273,6 +273,58 @@ def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool, layer:
     return res
 
 
+GEMM_SHAPES = [
+    # (name, n, k, epilogue) of the encoder's four projections, at the forward's M = 21,405
+    # valid tokens (the mean of the encoder workload's packed batch)
+    ("qkv_2304x768", 2304, 768, "none"),
+    ("wo_768x768_residual", 768, 768, "residual"),
+    ("geglu_wi_6144x768", 3072, 768, "geglu"),
+    ("mlp_wo_768x3072_residual", 768, 3072, "residual"),
+]
+GEMM_M = 21405
+
+
+def bench_gemms(steps: int, warmup: int) -> dict:
+    """The encoder's four GEMM shapes alone, with their fused epilogues, inputs resident in
+    HBM: K back-to-back launches per shape bracketed by one event pair on the launch stream."""
+    import torch
+
+    import raya_amd as R
+    from raya_amd import _capi as C
+
+    g = R.HipGemm()
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device="cuda").manual_seed(1000 * 4 + 7)
+    res = {"m": GEMM_M, "steps": steps, "warmup": warmup, "shapes": {}}
+    for name, n, k, epi in GEMM_SHAPES:
+        rows = 2 * n if epi == "geglu" else n
+        a = torch.randn(GEMM_M, k, device="cuda", generator=gen)
+        b = 0.02 * torch.randn(rows, k, device="cuda", generator=gen)
+        out = torch.randn(GEMM_M, n, device="cuda", generator=gen)
+        act = C.RAYA_EPI_GEGLU if epi == "geglu" else C.RAYA_EPI_NONE
+        resid = out if epi == "residual" else None
+
+        def step():
+            g.matmul_nt_device(out, a, b, activation=act, residual=resid, stream=stream)
+
+        for _ in range(warmup):
+            step()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        flops = 2.0 * GEMM_M * rows * k
+        res["shapes"][name] = {"n_out": n, "k": k, "epilogue": epi, "ms": ms,
+                               "tflops": flops / ms / 1e9,
+                               "mfma_frac": flops / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS}
+        del a, b, out
+    return res
+
+
 def bench_layer(m, steps: int, warmup: int) -> dict:
     """One block-local encoder layer (pre-LN, QKV + RoPE, BlockDiag(64) attention, Wo + residual,
     LN, GeGLU, Wo + residual) on B=16 x L=1024 valid tokens: the per-layer event spans of the
@@ -364,6 +416,8 @@ def main() -> int:
     ap.add_argument("--no-encoder", action="store_true", help="skip the encoder forward leg")
     ap.add_argument("--encoder-steps", type=int, default=10)
     ap.add_argument("--encoder-warmup", type=int, default=2)
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time only the encoder's four GEMM shapes and print their line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
@@ -374,6 +428,18 @@ def main() -> int:
     import torch
 
     import raya_amd as R
+
+    if args.gemm_only:
+        gm = bench_gemms(args.steps, args.warmup)
+        # one layer's four projections: total FLOP over total time
+        flop = sum(2.0 * GEMM_M * (2 * n if e == "geglu" else n) * k for _, n, k, e in GEMM_SHAPES)
+        ms = sum(v["ms"] for v in gm["shapes"].values())
+        print(json.dumps({"metric": "fp32 encoder GEMM TFLOP/s (one layer's four projections), 1 GPU",
+                          "value": flop / ms / 1e9, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+                          "warmup": args.warmup, "higher_is_better": True, "dtype": "f32",
+                          "data": "synthetic", "config": {"workload": "encoder_gemms_m21405"},
+                          "gemms": gm}), flush=True)
+        return 0
 
     wl = WORKLOADS[args.workload]
     b, h, s, d, mask_spec = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"], wl["mask"]
@@ -487,6 +553,8 @@ def main() -> int:
         result["encoder"] = enc
         if layer is not None:
             result["encoder_layer"] = layer
+        log("encoder gemm shapes")
+        result["encoder_gemms"] = bench_gemms(20, 3)
     print(json.dumps(result), flush=True)
     return 0
 
