@@ -216,54 +216,56 @@ constexpr int kMinWaves = DP <= 64 ? 4 : DP == 128 ? 2 : 1;
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
 // The first tile's loads at head_dim 64, as one block the compiler cannot
-// split: 4 K DMAs (16 bytes per lane each, LDS address in m0), the lane's 4 Q
-// chunks into registers, 4 V DMAs, then a wait until only the V DMAs may be
-// outstanding (loads complete in issue order).  Written as one asm statement so
+// split: 4 K DMAs (16 bytes per lane each, LDS address in m0, source a scalar
+// base plus a 32-bit per-lane byte offset), the lane's 4 Q chunks into
+// registers, 4 V DMAs, then a wait until only the V DMAs may be outstanding
+// (loads complete in issue order).  Written as one asm statement so
 // that the compiler neither waits for the V DMA before reading the K tile (it
 // cannot tell the two LDS tiles apart) nor touches q before the wait.
-__device__ __forceinline__ void issue_kqv64(const float *const ka[4], const uint32_t kl[4], const float *qa,
-                                            floatx4 q[4], const float *const va[4], const uint32_t vl[4]) {
+__device__ __forceinline__ void issue_kqv64(const float *kbase, const uint32_t ko[4], const uint32_t kl[4],
+                                            const float *qa, floatx4 q[4], const float *vbase,
+                                            const uint32_t vo[4], const uint32_t vl[4]) {
     asm volatile(
-        "s_mov_b32 m0, %[kl0]\n\tglobal_load_lds_dwordx4 %[ka0], off\n\t"
-        "s_mov_b32 m0, %[kl1]\n\tglobal_load_lds_dwordx4 %[ka1], off\n\t"
-        "s_mov_b32 m0, %[kl2]\n\tglobal_load_lds_dwordx4 %[ka2], off\n\t"
-        "s_mov_b32 m0, %[kl3]\n\tglobal_load_lds_dwordx4 %[ka3], off\n\t"
+        "s_mov_b32 m0, %[kl0]\n\tglobal_load_lds_dwordx4 %[ko0], %[kb]\n\t"
+        "s_mov_b32 m0, %[kl1]\n\tglobal_load_lds_dwordx4 %[ko1], %[kb]\n\t"
+        "s_mov_b32 m0, %[kl2]\n\tglobal_load_lds_dwordx4 %[ko2], %[kb]\n\t"
+        "s_mov_b32 m0, %[kl3]\n\tglobal_load_lds_dwordx4 %[ko3], %[kb]\n\t"
         "global_load_dwordx4 %[q0], %[qa], off\n\t"
         "global_load_dwordx4 %[q1], %[qa], off offset:16\n\t"
         "global_load_dwordx4 %[q2], %[qa], off offset:32\n\t"
         "global_load_dwordx4 %[q3], %[qa], off offset:48\n\t"
-        "s_mov_b32 m0, %[vl0]\n\tglobal_load_lds_dwordx4 %[va0], off\n\t"
-        "s_mov_b32 m0, %[vl1]\n\tglobal_load_lds_dwordx4 %[va1], off\n\t"
-        "s_mov_b32 m0, %[vl2]\n\tglobal_load_lds_dwordx4 %[va2], off\n\t"
-        "s_mov_b32 m0, %[vl3]\n\tglobal_load_lds_dwordx4 %[va3], off\n\t"
+        "s_mov_b32 m0, %[vl0]\n\tglobal_load_lds_dwordx4 %[vo0], %[vb]\n\t"
+        "s_mov_b32 m0, %[vl1]\n\tglobal_load_lds_dwordx4 %[vo1], %[vb]\n\t"
+        "s_mov_b32 m0, %[vl2]\n\tglobal_load_lds_dwordx4 %[vo2], %[vb]\n\t"
+        "s_mov_b32 m0, %[vl3]\n\tglobal_load_lds_dwordx4 %[vo3], %[vb]\n\t"
         "s_waitcnt vmcnt(4)"
         : [q0] "=&v"(q[0]), [q1] "=&v"(q[1]), [q2] "=&v"(q[2]), [q3] "=&v"(q[3])
-        : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [kl0] "s"(kl[0]),
-          [kl1] "s"(kl[1]), [kl2] "s"(kl[2]), [kl3] "s"(kl[3]), [qa] "v"(qa), [va0] "v"(va[0]),
-          [va1] "v"(va[1]), [va2] "v"(va[2]), [va3] "v"(va[3]), [vl0] "s"(vl[0]), [vl1] "s"(vl[1]),
-          [vl2] "s"(vl[2]), [vl3] "s"(vl[3])
+        : [kb] "s"(kbase), [ko0] "v"(ko[0]), [ko1] "v"(ko[1]), [ko2] "v"(ko[2]), [ko3] "v"(ko[3]),
+          [kl0] "s"(kl[0]), [kl1] "s"(kl[1]), [kl2] "s"(kl[2]), [kl3] "s"(kl[3]), [qa] "v"(qa),
+          [vb] "s"(vbase), [vo0] "v"(vo[0]), [vo1] "v"(vo[1]), [vo2] "v"(vo[2]), [vo3] "v"(vo[3]),
+          [vl0] "s"(vl[0]), [vl1] "s"(vl[1]), [vl2] "s"(vl[2]), [vl3] "s"(vl[3])
         : "memory", "m0");
 }
 
 // A later tile at head_dim 64: 4 K DMAs, 4 V DMAs, wait until only V may be
 // outstanding.
-__device__ __forceinline__ void issue_kv64(const float *const ka[4], const uint32_t kl[4],
-                                           const float *const va[4], const uint32_t vl[4]) {
+__device__ __forceinline__ void issue_kv64(const float *kbase, const uint32_t ko[4], const uint32_t kl[4],
+                                           const float *vbase, const uint32_t vo[4], const uint32_t vl[4]) {
     asm volatile(
-        "s_mov_b32 m0, %[kl0]\n\tglobal_load_lds_dwordx4 %[ka0], off\n\t"
-        "s_mov_b32 m0, %[kl1]\n\tglobal_load_lds_dwordx4 %[ka1], off\n\t"
-        "s_mov_b32 m0, %[kl2]\n\tglobal_load_lds_dwordx4 %[ka2], off\n\t"
-        "s_mov_b32 m0, %[kl3]\n\tglobal_load_lds_dwordx4 %[ka3], off\n\t"
-        "s_mov_b32 m0, %[vl0]\n\tglobal_load_lds_dwordx4 %[va0], off\n\t"
-        "s_mov_b32 m0, %[vl1]\n\tglobal_load_lds_dwordx4 %[va1], off\n\t"
-        "s_mov_b32 m0, %[vl2]\n\tglobal_load_lds_dwordx4 %[va2], off\n\t"
-        "s_mov_b32 m0, %[vl3]\n\tglobal_load_lds_dwordx4 %[va3], off\n\t"
+        "s_mov_b32 m0, %[kl0]\n\tglobal_load_lds_dwordx4 %[ko0], %[kb]\n\t"
+        "s_mov_b32 m0, %[kl1]\n\tglobal_load_lds_dwordx4 %[ko1], %[kb]\n\t"
+        "s_mov_b32 m0, %[kl2]\n\tglobal_load_lds_dwordx4 %[ko2], %[kb]\n\t"
+        "s_mov_b32 m0, %[kl3]\n\tglobal_load_lds_dwordx4 %[ko3], %[kb]\n\t"
+        "s_mov_b32 m0, %[vl0]\n\tglobal_load_lds_dwordx4 %[vo0], %[vb]\n\t"
+        "s_mov_b32 m0, %[vl1]\n\tglobal_load_lds_dwordx4 %[vo1], %[vb]\n\t"
+        "s_mov_b32 m0, %[vl2]\n\tglobal_load_lds_dwordx4 %[vo2], %[vb]\n\t"
+        "s_mov_b32 m0, %[vl3]\n\tglobal_load_lds_dwordx4 %[vo3], %[vb]\n\t"
         "s_waitcnt vmcnt(4)"
         :
-        : [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [kl0] "s"(kl[0]),
-          [kl1] "s"(kl[1]), [kl2] "s"(kl[2]), [kl3] "s"(kl[3]), [va0] "v"(va[0]), [va1] "v"(va[1]),
-          [va2] "v"(va[2]), [va3] "v"(va[3]), [vl0] "s"(vl[0]), [vl1] "s"(vl[1]), [vl2] "s"(vl[2]),
-          [vl3] "s"(vl[3])
+        : [kb] "s"(kbase), [ko0] "v"(ko[0]), [ko1] "v"(ko[1]), [ko2] "v"(ko[2]), [ko3] "v"(ko[3]),
+          [kl0] "s"(kl[0]), [kl1] "s"(kl[1]), [kl2] "s"(kl[2]), [kl3] "s"(kl[3]),
+          [vb] "s"(vbase), [vo0] "v"(vo[0]), [vo1] "v"(vo[1]), [vo2] "v"(vo[2]), [vo3] "v"(vo[3]),
+          [vl0] "s"(vl[0]), [vl1] "s"(vl[1]), [vl2] "s"(vl[2]), [vl3] "s"(vl[3])
         : "memory", "m0");
 }
 
@@ -507,14 +509,20 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // waited for after QK^T and the softmax.
     float qreg[DQ];
     // Operands of one tile's asm issue: this wave's K and V source rows and LDS slots.
-    const auto tile_addrs = [&](int kt, const float *ka[4], uint32_t kl[4], const float *va[4], uint32_t vl[4]) {
+    // Operands of one tile's asm issue: scalar bases at the tile's first row, 32-bit
+    // byte offsets of this wave's chunks (rows past the tile's keys clamped to its
+    // last row) and the LDS slots.
+    const auto tile_addrs = [&](int kt, const float *&kbase, uint32_t ko[4], uint32_t kl[4],
+                                const float *&vbase, uint32_t vo[4], uint32_t vl[4]) {
+        const int last = min(kt + kKeys, it.k_hi) - 1 - kt;
+        kbase = kb + (int64_t)kt * a.k_rs;
+        vbase = vb + (int64_t)kt * a.v_rs;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int slot = (wave * LPW + j) * 64 + lane;
-            const int r = slot / CH, c = swz<CH>(slot % CH, r);
-            const int64_t row = min(kt + r, min(kt + kKeys, it.k_hi) - 1);
-            ka[j] = kb + row * a.k_rs + 4 * c;
-            va[j] = vb + row * a.v_rs + 4 * c;
+            const int r = min(slot / CH, last), c = swz<CH>(slot % CH, slot / CH);
+            ko[j] = (uint32_t)(r * (int)a.k_rs * 4 + 16 * c);
+            vo[j] = (uint32_t)(r * (int)a.v_rs * 4 + 16 * c);
             const int lds_off = (wave * LPW + j) * 64 * 16;
             kl[j] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)((char *)ks + lds_off));
             vl[j] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)((char *)vs + lds_off));
@@ -522,12 +530,12 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     };
     if constexpr (FUSED) {
         // K, Q and V in one asm block that ends waiting for K and Q only.
-        const float *ka[4], *va[4];
-        uint32_t kl[4], vl[4];
-        tile_addrs(it.k_lo, ka, kl, va, vl);
+        const float *kbase, *vbase;
+        uint32_t ko[4], kl[4], vo[4], vl[4];
+        tile_addrs(it.k_lo, kbase, ko, kl, vbase, vo, vl);
         const float *qa = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)min(qi, valid - 1) * a.q_rs + g * DQ;
         floatx4 q4[4];
-        issue_kqv64(ka, kl, qa, q4, va, vl);
+        issue_kqv64(kbase, ko, kl, qa, q4, vbase, vo, vl);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -563,10 +571,10 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             // Every wave's LDS reads of the previous tile have returned.
             barrier_after_reads();
             if constexpr (FUSED) {
-                const float *ka[4], *va[4];
-                uint32_t kl[4], vl[4];
-                tile_addrs(kt, ka, kl, va, vl);
-                issue_kv64(ka, kl, va, vl);
+                const float *kbase, *vbase;
+                uint32_t ko[4], kl[4], vo[4], vl[4];
+                tile_addrs(kt, kbase, ko, kl, vbase, vo, vl);
+                issue_kv64(kbase, ko, kl, vbase, vo, vl);
             } else {
                 stage(kb, a.k_rs, ks, kt);
                 stage(vb, a.v_rs, vs, kt);
@@ -670,6 +678,8 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_timed_kernel(c
     }
 }
 
+constexpr int64_t kMaxFusedRowStride = (int64_t(1) << 31) / (4 * kKeys) - kKeys;  // floats
+
 // Half the bit width of the scatter domain: the smallest h with 4^h >= total.
 int scatter_half_bits(int64_t total) {
     int h = 1;
@@ -706,7 +716,12 @@ hipError_t launch_attention(const AttnLaunch &a, hipStream_t stream) {
     case 16: return launch_dp<16>(a, stream);
     case 32: return launch_dp<32>(a, stream);
     case 48: return launch_dp<48>(a, stream);
-    case 64: return a.head_dim == 64 ? launch_dp<64, true>(a, stream) : launch_dp<64>(a, stream);
+    case 64:
+        // The fused issue forms K/V offsets within a tile in 32 bits: 63 rows of the
+        // row stride plus the last chunk must stay below 2^31 bytes.
+        return a.head_dim == 64 && a.k_rs < kMaxFusedRowStride && a.v_rs < kMaxFusedRowStride
+                   ? launch_dp<64, true>(a, stream)
+                   : launch_dp<64>(a, stream);
     case 80: return launch_dp<80>(a, stream);
     case 96: return launch_dp<96>(a, stream);
     case 112: return launch_dp<112>(a, stream);

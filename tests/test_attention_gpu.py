@@ -337,3 +337,27 @@ def test_random_sweep_against_the_oracle(hip_attention):
         check_close(got, want, f"case {case}")
         for i in range(b):
             assert (got[i, :, clamped[i]:, :] == 0).all()
+
+
+def test_row_strides_past_the_fused_offset_range(hip_attention):
+    """head_dim 64 with a row stride of 8.4M floats (33.6 MB per row): past what the fused
+    issue's 32-bit in-tile offsets hold, so the launch takes the general head_dim-64 kernel;
+    it matches the oracle like the dense layout does."""
+    s, d, rs = 3, 64, 8_400_000
+    rng = np.random.default_rng(5)
+    q, k, v = (rng.standard_normal((1, 1, s, d)).astype(np.float32) for _ in range(3))
+    bufs = []
+    for x in (q, k, v):
+        t = torch.zeros(s * rs, device="cuda")
+        t.view(s, rs)[:, :d] = _dev(x[0, 0])
+        bufs.append(t)
+    out = torch.full((s * rs,), float("nan"), device="cuda")
+    lay = {"shape": (1, 1, s, d), "q": (0, 0, rs), "k": (0, 0, rs), "v": (0, 0, rs), "out": (0, 0, rs)}
+    for name in ("full", "window64"):
+        mask, okind, block, window = MASKS[name]
+        hip_attention.attend_batched(*bufs, out, _dev(np.array([s], np.int32)), mask, layouts=lay)
+        torch.cuda.synchronize()
+        got = out.view(s, rs)[:, :d].cpu().numpy()
+        want = oracle.naive_attend_batched(q, k, v, okind, np.array([s], np.int32),
+                                           R.kernels.default_scale(d), block=block, window=window)
+        check_close(got, want[0, 0], name)
