@@ -156,8 +156,18 @@ __global__ void head_finish_kernel(const float *raw_logits, const uint8_t *mask,
                                    int markers, const float *h, int64_t ldh,
                                    const int32_t *seq_start, int d, float *logits, float *probs,
                                    float *features, float *pooled, float *act_in) {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    // One workgroup per sequence: every thread copies part of the CLS row; thread 0
+    // runs the marker softmax and the features in the reference's sequential order.
+    const int b = blockIdx.x;
     if (b >= batch) return;
+    const float *row0 = h + (int64_t)seq_start[b] * ldh;
+    float *ai = act_in + (int64_t)b * (d + 4);
+    for (int c = threadIdx.x; c < d; c += blockDim.x) {
+        const float x = row0[c];
+        pooled[(int64_t)b * d + c] = x;
+        ai[c] = x;
+    }
+    if (threadIdx.x != 0) return;
     const float *raw = raw_logits + (int64_t)b * markers;
     const uint8_t *mk = mask + (int64_t)b * markers;
     float *lg = logits + (int64_t)b * markers;
@@ -189,12 +199,6 @@ __global__ void head_finish_kernel(const float *raw_logits, const uint8_t *mask,
     }
     if (markers < 2) top2 = 0.0f;
     float f[4] = {top1, __fsub_rn(top1, top2), __fdiv_rn(-ent, logf(k)), __fdiv_rn(k, 255.0f)};
-    const float *row0 = h + (int64_t)seq_start[b] * ldh;
-    float *ai = act_in + (int64_t)b * (d + 4);
-    for (int c = 0; c < d; ++c) {
-        pooled[(int64_t)b * d + c] = row0[c];
-        ai[c] = row0[c];
-    }
     for (int c = 0; c < 4; ++c) {
         features[b * 4 + c] = f[c];
         ai[d + c] = f[c];
@@ -257,7 +261,7 @@ hipError_t launch_head_finish(const float *raw_logits, const uint8_t *mask, int 
                               float *logits, float *probs, float *features, float *pooled,
                               float *act_in, hipStream_t stream) {
     if (batch == 0) return hipSuccess;
-    hipLaunchKernelGGL(head_finish_kernel, dim3(blocks_for(batch, 64)), dim3(64), 0, stream,
+    hipLaunchKernelGGL(head_finish_kernel, dim3((unsigned)batch), dim3(256), 0, stream,
                        raw_logits, mask, batch, markers, h, ldh, seq_start, d, logits, probs,
                        features, pooled, act_in);
     return hipGetLastError();
