@@ -642,19 +642,24 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     }
     l = sum_xor32(sum_xor16(l));
 
-    // Register r of oacc[n] holds dim g DQ + NT r + n of row qi; rows at or
-    // beyond valid hold zeros (every key was masked) and are stored as such.
+    // Register r of oacc[n] holds dim g DQ + NT r + n of row qi.  Rows at or
+    // beyond valid, and rows with no weight, are stored as literal zeros: their
+    // accumulators are zero weights times V, which is NaN wherever V is not
+    // finite.
     if (qi < (packed ? valid : a.seq)) {
-        const float inv = (qi < valid && l > 0.f) ? 1.f / l : 0.f;
+        const bool zero_row = !(qi < valid && l > 0.f);
+        const float inv = zero_row ? 0.f : 1.f / l;
         float *orow = ob + (int64_t)qi * a.o_rs + g * DQ;
 #pragma unroll
         for (int c = 0; c < DQ / 4; ++c) {
             if (g * DQ + 4 * c < D) {
-                float4 y;
-                y.x = oacc[(4 * c + 0) % NT][(4 * c + 0) / NT] * inv;
-                y.y = oacc[(4 * c + 1) % NT][(4 * c + 1) / NT] * inv;
-                y.z = oacc[(4 * c + 2) % NT][(4 * c + 2) / NT] * inv;
-                y.w = oacc[(4 * c + 3) % NT][(4 * c + 3) / NT] * inv;
+                float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (!zero_row) {
+                    y.x = oacc[(4 * c + 0) % NT][(4 * c + 0) / NT] * inv;
+                    y.y = oacc[(4 * c + 1) % NT][(4 * c + 1) / NT] * inv;
+                    y.z = oacc[(4 * c + 2) % NT][(4 * c + 2) / NT] * inv;
+                    y.w = oacc[(4 * c + 3) % NT][(4 * c + 3) / NT] * inv;
+                }
                 *(float4 *)(orow + 4 * c) = y;
             }
         }

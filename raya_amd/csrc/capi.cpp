@@ -53,10 +53,12 @@ int ok() {
 
 namespace {
 
-// Mask and parameter checks shared by both attention entry points.  The first
-// four checks restate validate() (attention.rs:128-158) in its order.
-int check_attn(uint64_t heads, uint64_t seq, uint64_t head_dim, int32_t kind,
-               uint64_t mask_arg, uint64_t block, const uint64_t *valid_len) {
+// validate() (attention.rs:128-158) in its order: shape, head_dim, valid_len,
+// block.  The buffer lengths (attention.rs:159-168) come next, checked by the
+// host-slice entry points, and only then the limits of the HIP kernel
+// (check_hip_limits), which the reference has no counterpart for.
+int check_attn(uint64_t heads, uint64_t head_dim, uint64_t seq, uint64_t block,
+               const uint64_t *valid_len) {
     if (heads == 0 || head_dim == 0) return fail(RAYA_ERR_SHAPE, "invalid shape: heads and head_dim must be at least 1");
     if (head_dim % 8 != 0)
         return fail(RAYA_ERR_SHAPE, "invalid shape: head_dim %" PRIu64 " is not a multiple of 8", head_dim);
@@ -65,6 +67,11 @@ int check_attn(uint64_t heads, uint64_t seq, uint64_t head_dim, int32_t kind,
     if (block != RAYA_BLOCK)
         return fail(RAYA_ERR_UNSUPPORTED, "unsupported: block %" PRIu64 " (only %d is supported)", block,
                     RAYA_BLOCK);
+    return RAYA_OK;
+}
+
+// The mask extension and the kernel's instantiated limits.
+int check_hip_limits(uint64_t heads, uint64_t seq, uint64_t head_dim, int32_t kind, uint64_t mask_arg) {
     if (kind < RAYA_MASK_BLOCK3 || kind > RAYA_MASK_BLOCKDIAG)
         return fail(RAYA_ERR_UNSUPPORTED, "unsupported: mask kind %d", kind);
     if (kind == RAYA_MASK_BLOCKDIAG && mask_arg == 0)
@@ -133,16 +140,21 @@ static int attend_host(const raya_attn_shape *shape, const raya_attn_params *par
                        size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
                        float *out, size_t out_len, raya_stage_cycles *stages) {
     if (!shape || !params) return fail(RAYA_ERR_SHAPE, "invalid shape: null shape or params");
-    int rc = check_attn(shape->heads, shape->seq, shape->head_dim, params->mask_kind,
-                        params->mask_arg, params->block, &params->valid_len);
+    int rc = check_attn(shape->heads, shape->head_dim, shape->seq, params->block, &params->valid_len);
     if (rc) return rc;
-    const uint64_t numel = shape->heads * shape->seq * shape->head_dim;
+    // AttnShape::numel (attention.rs:81-83); a product past 2^64 matches no buffer.
+    uint64_t numel = 0;
+    if (__builtin_mul_overflow(shape->heads, shape->seq, &numel) ||
+        __builtin_mul_overflow(numel, shape->head_dim, &numel))
+        return fail(RAYA_ERR_SHAPE, "invalid shape: heads x seq x head_dim overflows 64 bits");
     const struct {
         const char *name;
         size_t len;
     } bufs[4] = {{"q", q_len}, {"k", k_len}, {"v", v_len}, {"out", out_len}};
     for (const auto &bf : bufs)
         if (bf.len != numel) return fail_length(bf.name, bf.len, numel);
+    rc = check_hip_limits(shape->heads, shape->seq, shape->head_dim, params->mask_kind, params->mask_arg);
+    if (rc) return rc;
     if (stages) *stages = raya_stage_cycles{};
     if (numel == 0) return ok();
     if (!q || !k || !v || !out) return fail(RAYA_ERR_SHAPE, "invalid shape: null buffer");
@@ -237,7 +249,8 @@ namespace {
 int attend_batched(const raya_attn_batch *d, const int32_t *valid_len, const float *q, const float *k,
                    const float *v, float *out, raya_stage_cycles *stages, void *stream) {
     if (!d) return fail(RAYA_ERR_SHAPE, "invalid shape: null descriptor");
-    int rc = check_attn(d->heads, d->seq, d->head_dim, d->mask_kind, d->mask_arg, d->block, nullptr);
+    int rc = check_attn(d->heads, d->head_dim, d->seq, d->block, nullptr);
+    if (!rc) rc = check_hip_limits(d->heads, d->seq, d->head_dim, d->mask_kind, d->mask_arg);
     if (rc) return rc;
     if (d->batch > 0x7fffffffu) return fail(RAYA_ERR_UNSUPPORTED, "unsupported: batch %" PRIu64, d->batch);
     if (d->batch == 0 || d->seq == 0) return ok();

@@ -341,17 +341,38 @@ class HipGemm(GemmBackend):
         """out[m, n] = act(a[m, k] @ b[n, k]^T + bias) + residual on GPU tensors.
         For GEGLU, b is [2n, k] and bias [2n].  Row strides are taken from the
         tensors (last dimension must be contiguous)."""
-        m, k = a.shape
-        n = out.shape[1]
+        import torch
+
+        # Every operand is checked before anything reaches the device: another
+        # dtype, a short bias or a host tensor would hand the kernel fewer bytes
+        # than it reads, or a pointer it cannot read.  Shapes and dtypes first,
+        # the device last.
+        named = [("out", out), ("a", a), ("b", b)]
+        named += [(n_, t) for n_, t in (("bias", bias), ("residual", residual)) if t is not None]
+        for name, t in named:
+            if not isinstance(t, torch.Tensor):
+                raise TypeError(f"`{name}` must be a torch tensor")
+            if t.dtype != torch.float32:
+                raise TypeError(f"`{name}` must be float32")
         for name, t in (("out", out), ("a", a), ("b", b)):
             if t.dim() != 2 or t.stride(1) != 1:
                 raise ShapeError(f"invalid shape: `{name}` must be 2-D with contiguous rows")
+        m, k = a.shape
+        n = out.shape[1]
         rows_b = 2 * n if activation == C.RAYA_EPI_GEGLU else n
         if tuple(b.shape) != (rows_b, k) or out.shape[0] != m:
             raise ShapeError("invalid shape: operands do not agree")
+        if bias is not None and (bias.dim() != 1 or bias.numel() != rows_b or not bias.is_contiguous()):
+            raise ShapeError(f"invalid shape: `bias` must be a contiguous vector of {rows_b} entries")
+        if residual is not None and (residual.dim() != 2 or tuple(residual.shape) != (m, n)
+                                     or residual.stride(1) != 1):
+            raise ShapeError("invalid shape: `residual` must be [m, n] with contiguous rows")
+        for name, t in named:
+            if not t.is_cuda:
+                raise TypeError(f"`{name}` must be a torch tensor on the GPU")
         ep = C.GemmEpilogueC(activation, 0,
-                             ctypes.c_void_p(bias.data_ptr()) if bias is not None else None,
-                             ctypes.c_void_p(residual.data_ptr()) if residual is not None else None,
+                             _dev_ptr(bias, "bias") if bias is not None else None,
+                             _dev_ptr(residual, "residual") if residual is not None else None,
                              residual.stride(0) if residual is not None else 0)
         rc = C.lib().raya_matmul_nt_device(_dev_ptr(out, "out"), out.stride(0), _dev_ptr(a, "a"),
                                            a.stride(0), _dev_ptr(b, "b"), b.stride(0), m, n, k,

@@ -361,3 +361,32 @@ def test_row_strides_past_the_fused_offset_range(hip_attention):
         want = oracle.naive_attend_batched(q, k, v, okind, np.array([s], np.int32),
                                            R.kernels.default_scale(d), block=block, window=window)
         check_close(got, want[0, 0], name)
+
+
+def test_non_finite_v_outside_a_window(hip_attention):
+    """An Inf in V at key j (dim c) under Window64.  The reference sums over each row's own
+    key range only (naive.rs:13-65), so rows whose window holds j get Inf in dim c and every
+    other row stays finite.  Here the PV product runs over whole 16-key subtiles on the
+    matrix core, so a row whose window excludes j but whose workgroup's subtiles include it
+    gets 0 x Inf = NaN in dim c (and only there).  Pinned: rows with j in their window are
+    +Inf in dim c and match the oracle elsewhere; every other row matches the oracle in every
+    dim but c, where it is the oracle's value or NaN; padded rows are exact zeros."""
+    h, s, d, valid, j, c = 2, 512, 64, 400, 200, 5
+    q, k, v = oracle.qkv(h, s, d, 77)
+    v = v.copy()
+    v[:, j, c] = np.inf
+    for mask, okind in ((R.Mask.WINDOW64, oracle.MASK_WINDOW64), (R.Mask.sliding(64), oracle.MASK_SLIDING)):
+        got = run_hip(hip_attention, q, k, v, mask, valid, fill=np.nan)
+        want = oracle_naive(q, k, v, okind, valid, 128, 64)
+        assert (got[:, valid:] == 0).all(), "padded rows must be literal zeros"
+        sees = np.abs(np.arange(valid) - j) <= 64
+        others = [x for x in range(d) if x != c]
+        assert (got[:, :valid][:, sees, c] == np.inf).all()
+        assert (want[:, :valid][:, sees, c] == np.inf).all()
+        check_close(got[:, :valid][..., others], want[:, :valid][..., others], mask.name())
+        gc, wc = got[:, :valid][:, ~sees, c], want[:, :valid][:, ~sees, c]
+        assert np.isfinite(wc).all()
+        same = np.isfinite(gc)
+        assert (np.isnan(gc) | same).all()
+        assert np.abs(gc[same] - wc[same]).max() < MAX_ABS
+        print(f"{mask.name()}: {int((~same).sum())} of {gc.size} rows outside the window are NaN in dim {c}")

@@ -9,6 +9,7 @@ import pytest
 
 import bench
 from raya_amd import Mask
+from raya_amd import workloads as W
 from tests.conftest import ROOT
 
 
@@ -21,13 +22,13 @@ def brute_pairs(mask, v):
                                        (("block3",), Mask.BLOCK3), (("window64",), Mask.WINDOW64)])
 @pytest.mark.parametrize("v", [0, 1, 63, 64, 65, 127, 128, 129, 300, 512, 1000, 2048])
 def test_key_pairs_match_key_range(spec, mask, v):
-    assert bench.key_pairs(spec, v) == brute_pairs(mask, v)
+    assert W.key_pairs(spec, v) == brute_pairs(mask, v)
 
 
 def test_algorithmic_flop_and_bytes():
     valid = np.array([512, 700, 2048], np.int32)
     h, d, s = 12, 64, 2048
-    flops, nbytes = bench.algorithmic(valid, h, d, s, ("block_diag", 64))
+    flops, nbytes = W.algorithmic(valid, h, d, s, ("block_diag", 64))
     pairs = sum(brute_pairs(Mask.block_diag(64), int(v)) for v in valid)
     assert flops == 4 * d * h * pairs
     assert nbytes == 4 * (3 * h * d * int(valid.sum()) + len(valid) * h * s * d)
@@ -37,10 +38,10 @@ def test_headline_workload_figures():
     """The default workload's per-launch figures quoted in the profiles."""
     from raya_amd import synth
 
-    wl = bench.WORKLOADS[bench.DEFAULT]
+    wl = W.ATTENTION[W.DEFAULT_ATTENTION]
     lo, hi = wl["valid"]  # the valid lengths make_inputs draws, without the Q/K/V tensors
-    valid = synth.integers(synth.workload_seed(wl["config"], 3), wl["batch"], lo, hi)
-    flops, nbytes = bench.algorithmic(valid, wl["heads"], wl["head_dim"], wl["seq"], wl["mask"])
+    valid = synth.integers(synth.workload_seed(wl["family"], 3), wl["batch"], lo, hi)
+    flops, nbytes = W.algorithmic(valid, wl["heads"], wl["head_dim"], wl["seq"], wl["mask"])
     assert (flops, nbytes) == (7_387_216_896, 550_548_480)
 
 

@@ -166,3 +166,59 @@ def test_header_builds_a_plain_c_client(tmp_path):
     assert (name, gemm) == ("hip-gfx950", "hip-gfx950-mfma")
     assert int(rc) == int(code) == C.RAYA_ERR_SHAPE
     assert msg.startswith("invalid shape")
+
+
+def test_length_before_hip_limits():
+    """validate() checks the buffer lengths right after the block (attention.rs:159-168),
+    before anything the HIP kernel adds: head_dim 136 (past the kernel's 128) with a short
+    `q` is a Length error, as the reference gives."""
+    k = R.HipAttention()
+    shape = R.AttnShape(1, 2, 136)
+    buf = _ok(shape)
+    with pytest.raises(R.LengthError) as e:
+        k.attend(shape, R.AttnParams.new(R.Mask.WINDOW64, 2, 136), buf[:5], buf, buf, _ok(shape))
+    assert (e.value.name, e.value.got, e.value.expected) == ("q", 5, 272)
+    # the mask extension's own check also comes after the lengths
+    s8 = R.AttnShape(1, 4, 8)
+    with pytest.raises(R.LengthError):
+        k.attend(s8, R.AttnParams.new(R.Mask.block_diag(0), 4, 8), _ok(s8), _ok(s8)[:1], _ok(s8), _ok(s8))
+
+
+def test_numel_overflow_is_a_shape_error():
+    """heads x seq x head_dim past 2^64 cannot match any buffer and must not wrap into one."""
+    lib = C.lib()
+    s = C.AttnShapeC(1 << 32, 1 << 16, 1 << 16)
+    p = C.AttnParamsC(C.RAYA_MASK_FULL, 1.0, 0, 128, 0)
+    buf = (ctypes.c_float * 1)()
+    # the product is 2^64, which wraps to 0: zero-length buffers would "match" it
+    rc = lib.raya_attend(ctypes.byref(s), ctypes.byref(p), buf, 0, buf, 0, buf, 0, buf, 0)
+    assert rc == C.RAYA_ERR_SHAPE
+    assert "overflows" in C.last_error().message.decode()
+    assert C.last_error().code == rc
+
+
+def test_gemm_device_arguments_are_checked_before_any_launch():
+    """matmul_nt_device rejects another dtype, a short bias, a residual of the wrong shape
+    and host tensors before a pointer reaches the C ABI."""
+    import torch
+
+    g = R.HipGemm()
+    m, n, k = 4, 3, 8
+    a, b, out = torch.zeros(m, k), torch.zeros(n, k), torch.zeros(m, n)
+    with pytest.raises(TypeError, match="float32"):
+        g.matmul_nt_device(out, a.double(), b)
+    with pytest.raises(TypeError, match="float32"):
+        g.matmul_nt_device(out, a, b.half())
+    with pytest.raises(TypeError, match="float32"):
+        g.matmul_nt_device(out, a, b, bias=torch.zeros(n, dtype=torch.float64))
+    with pytest.raises(R.ShapeError, match="bias"):
+        g.matmul_nt_device(out, a, b, bias=torch.zeros(n - 1))
+    with pytest.raises(R.ShapeError, match="bias"):  # GeGLU needs 2n bias entries
+        g.matmul_nt_device(out, a, torch.zeros(2 * n, k), bias=torch.zeros(n),
+                           activation=C.RAYA_EPI_GEGLU)
+    with pytest.raises(R.ShapeError, match="residual"):
+        g.matmul_nt_device(out, a, b, residual=torch.zeros(m, n + 1))
+    with pytest.raises(R.ShapeError, match="residual"):
+        g.matmul_nt_device(out, a, b, residual=torch.zeros(n, m).t())
+    with pytest.raises(TypeError, match="GPU"):  # host tensors never reach the library
+        g.matmul_nt_device(out, a, b, bias=torch.zeros(n), residual=torch.zeros(m, n))
