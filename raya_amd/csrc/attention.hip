@@ -26,6 +26,8 @@
 // and B agree; it is chosen so that every operand is a contiguous LDS or HBM
 // read.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 
 #include "internal.hpp"
 #include "raya_hip.h"
@@ -38,6 +40,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQRows = 16 * kWaves;  // query rows per workgroup
+constexpr int kSplitRows = 16;       // query rows per workgroup of the split kernel
 constexpr int kKeys = 64;            // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -122,17 +125,18 @@ __device__ __forceinline__ int clamp_valid(const AttnLaunch &a, int b) {
     return min(max(valid, 0), a.seq);
 }
 
-// Item `item` of the (sequence, head, tile) order.
+// Item `item` of the (sequence, head, tile) order, tiles of ROWS query rows.
+template <int ROWS>
 __device__ __forceinline__ Item decode(const AttnLaunch &a, const Plan &p, int item) {
     Item it;
     const int bh = fdiv(item, p.by_qt);
     const int tile = item - bh * p.n_qt;
     it.b = fdiv(bh, p.by_heads);
     it.h = bh - it.b * a.heads;
-    it.q0 = tile * kQRows;
+    it.q0 = tile * ROWS;
     it.valid = clamp_valid(a, it.b);
     if (it.q0 < it.valid) {
-        const int qlast = min(it.q0 + kQRows, it.valid) - 1;
+        const int qlast = min(it.q0 + ROWS, it.valid) - 1;
         it.k_lo = key_range(a.mask_kind, a.mask_arg, p.by_arg, it.q0, it.valid).lo;
         it.k_hi = key_range(a.mask_kind, a.mask_arg, p.by_arg, qlast, it.valid).hi;
     } else {
@@ -391,6 +395,80 @@ __device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4
     }
 }
 
+// The split kernel's share of a tile: this wave's subtile t (keys 16t .. 16t + 15)
+// only.  S^T of the subtile against the lane's Q slice, register r of lane
+// (g, li) the raw score of key 16t + 4r + g.
+template <int DP>
+__device__ __forceinline__ floatx4 qk_sub(const float *ks, const float (&qreg)[DP / 4], int g, int k_row0, int t) {
+    constexpr int DQ = DP / 4, CH = DP / 4;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * t + k_row0;
+    const float *kp = ks + row * DP;
+#pragma unroll
+    for (int c = 0; c < DQ / 4; ++c) {
+        const float4 x = *(const float4 *)(kp + 4 * swz<CH>(g * (DQ / 4) + c, row));
+        acc = mfma(x.x, qreg[4 * c + 0], acc);
+        acc = mfma(x.y, qreg[4 * c + 1], acc);
+        acc = mfma(x.z, qreg[4 * c + 2], acc);
+        acc = mfma(x.w, qreg[4 * c + 3], acc);
+    }
+    return acc;
+}
+
+// softmax_tile for one subtile's four scores per lane (keys 16t + 4r + g); the
+// scores outside [lo, hi) (tile-relative, offset by g) are masked.
+template <int NT>
+__device__ __forceinline__ void softmax_sub(floatx4 &s, floatx4 (&oacc)[NT], float &m, float &l, int t, int lo, int hi,
+                                            float c_exp) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int j = 16 * t + 4 * r;
+        if (j < lo || j >= hi) s[r] = -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    tmax = max_xor32(max_xor16(tmax));
+    const float m_new = fmaxf(m, tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = fast_exp2((m - m_use) * c_exp);
+    l *= alpha;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) oacc[n] *= alpha;
+    m = m_new;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        s[r] = fast_exp2((s[r] - m_use) * c_exp);
+        l += s[r];
+    }
+}
+
+// O^T += V^T P^T over this wave's subtile t.
+template <int DP>
+__device__ __forceinline__ void pv_sub(const float *vs, const floatx4 &s, int g, int li, floatx4 (&oacc)[DP / 16],
+                                       int t) {
+    constexpr int NT = DP / 16, CH = DP / 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = 16 * t + 4 * r + g;
+        const float *vp = vs + row * DP;
+        float vop[NT];
+        if constexpr (NT == 4) {
+            const float4 x = *(const float4 *)(vp + 4 * swz<CH>(li, row));
+            vop[0] = x.x;
+            vop[1] = x.y;
+            vop[2] = x.z;
+            vop[3] = x.w;
+        } else {
+#pragma unroll
+            for (int n = 0; n < NT; ++n) {
+                const int d = NT * li + n;
+                vop[n] = vp[4 * swz<CH>(d >> 2, row) + (d & 3)];
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NT; ++n) oacc[n] = mfma(vop[n], s[r], oacc[n]);
+    }
+}
+
 // Stage clock of the instrumented kernel (raya_attend_batched_stages): the
 // shader clock (s_memtime) is read at each stage boundary of a tile and the
 // difference added to that stage's total.  The scheduling barriers keep the
@@ -439,10 +517,17 @@ __device__ __forceinline__ void lap(StageClock *c, uint64_t &bucket) {
 // has landed before its QK^T starts.  FUSED (head_dim exactly 64): every tile's
 // loads are issued by the asm blocks above with explicit waits, so V stays in
 // flight during QK^T and the softmax.
-template <int DP, bool FUSED, bool TIMED, bool SKIP = false>  // head_dim padded to a multiple of 16
+//
+// SPLIT: the item is 16 query rows and the four waves split every 64-key tile
+// between them, wave w taking its 16-key subtile w (the grids too small to
+// fill the chip: a quarter of the MFMA chain per wave).  Each wave keeps its
+// own running max, sum and output over its keys; at the end the four partial
+// states are combined through LDS, each wave finishing a quarter of the dims.
+template <int DP, bool FUSED, bool TIMED, bool SKIP = false, bool SPLIT = false>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs, StageClock *clk) {
     static_assert(!FUSED || DP == 64, "the fused issue is written for head_dim 64");
+    constexpr int ROWS = SPLIT ? kSplitRows : kQRows;
     constexpr int DQ = DP / 4;   // head-dim slice owned by one lane group
     constexpr int NT = DP / 16;  // 16-dim output tiles
     constexpr int CH = DP / 4;   // 16-byte chunks per row
@@ -457,11 +542,14 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     const int dch = D / 4;  // valid chunks per row
     const int kind = a.mask_kind, arg = a.mask_arg;
     // exp(scale * (x - y)) = exp2((x - y) * c) on raw dot products x, y; a
-    // negative scale is carried by negating Q, so c > 0 and max commutes.
-    const float c_exp = fabsf(a.scale) * kLog2e;
+    // negative scale is carried by negating Q, so c > 0 and max commutes.  c is
+    // kept at least FLT_MIN so that a masked key (x = -inf) weighs exactly 0
+    // even at scale 0 (-inf * 0 would be NaN); every finite (x - y) * FLT_MIN
+    // rounds to an exponent of 0, the uniform weights scale 0 asks for.
+    const float c_exp = fmaxf(fabsf(a.scale) * kLog2e, 1.17549435e-38f);
     const float q_sign = a.scale < 0.f ? -1.f : 1.f;
 
-    const Item it = decode(a, p, item_of(blockIdx.x, p));
+    const Item it = decode<ROWS>(a, p, item_of(blockIdx.x, p));
     // Packed sequences start at a row offset and have no padded rows in memory.
     const bool packed = a.seq_start != nullptr;
     const int64_t row0 = packed ? (int64_t)a.seq_start[it.b] : 0;
@@ -471,7 +559,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     float *ob = a.out + base(a.o_bs, a.o_hs, a.o_rs);
     if (it.k_lo >= it.k_hi) {  // every row is padding: write zeros
         if (packed) return;
-        for (int c = tid; c < kQRows * CH; c += kThreads) {
+        for (int c = tid; c < ROWS * CH; c += kThreads) {
             const int r = it.q0 + c / CH, c4 = c % CH;
             if (r < a.seq && c4 < dch)
                 *(float4 *)(ob + (int64_t)r * a.o_rs + 4 * c4) = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -479,7 +567,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         return;
     }
 
-    const int qw = it.q0 + wave * 16;
+    const int qw = SPLIT ? it.q0 : it.q0 + wave * 16;
     const int qi = qw + li;
     const int valid = it.valid;
     const Range rr = qi < valid ? key_range(kind, arg, p.by_arg, qi, valid) : Range{0, 0};
@@ -598,31 +686,59 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 for (int e = 0; e < 4; ++e) qreg[4 * c + e] = in ? qreg[4 * c + e] * q_sign : 0.f;
             }
         }
-        const bool active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
+        const bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
+        bool active = rows_active;
         // Sliding windows: the 16-key subtiles outside the union of the wave's
         // key intervals [w_first.lo, w_last.hi) hold no live key for any of its
         // rows (about a quarter of an item's subtiles at Window64); such a tile
         // always takes the masked softmax, which sets those scores to -inf.
+        // SPLIT keeps only the wave's own subtile.
         int live = 0xF;
-        if constexpr (SKIP) {
+        if constexpr (SKIP || SPLIT) {
             live = 0;
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 if (kt + 16 * t < w_last.hi && kt + 16 * t + 16 > w_first.lo) live |= 1 << t;
+            if constexpr (SPLIT) live &= 1 << wave;
             live = __builtin_amdgcn_readfirstlane(live);
+            if constexpr (SPLIT) active = active && live != 0;
+        }
+        // The keys this wave may score in this tile: the row's interval, and
+        // under SPLIT only its own subtile.
+        int m_lo = rr.lo, m_hi = rr.hi;
+        if constexpr (SPLIT) {
+            m_lo = max(m_lo, kt + 16 * wave);
+            m_hi = min(m_hi, kt + 16 * wave + 16);
         }
         floatx4 sacc[4];
-        if constexpr (TIMED) lap(clk, clk->load_wait);
+        floatx4 ssub;
+        if constexpr (TIMED) {
+            lap(clk, clk->load_wait);
+            // A split tile (16 rows x 64 keys) is computed by the four waves together.
+            if constexpr (SPLIT) clk->tiles += wave == 0 && rows_active;
+        }
         if (active) {
-            qk_tile<DP>(ks, qreg, g, k_row0, sacc, live);
-            if constexpr (TIMED) {
-                settle(sacc);
-                lap(clk, clk->qk);
-                ++clk->tiles;
+            if constexpr (SPLIT) {
+                ssub = qk_sub<DP>(ks, qreg, g, k_row0, wave);
+            } else {
+                qk_tile<DP>(ks, qreg, g, k_row0, sacc, live);
             }
-            softmax_tile<NT>(sacc, oacc, m, l, kt == it.k_lo,
-                             !(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi), rr.lo - kt - g,
-                             rr.hi - kt - g, c_exp);
+            if constexpr (TIMED) {
+                if constexpr (SPLIT) {
+                    settle(ssub[3]);
+                } else {
+                    settle(sacc);
+                    ++clk->tiles;
+                }
+                lap(clk, clk->qk);
+            }
+            if constexpr (SPLIT) {
+                softmax_sub<NT>(ssub, oacc, m, l, wave, m_lo - kt - g, m_hi - kt - g, c_exp);
+            } else {
+                softmax_tile<NT>(sacc, oacc, m, l, kt == it.k_lo,
+                                 !(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi), m_lo - kt - g,
+                                 m_hi - kt - g, c_exp);
+            }
             if constexpr (TIMED) {
                 settle(l);
                 settle(oacc);
@@ -633,7 +749,10 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         barrier_only();
         if constexpr (TIMED) lap(clk, clk->load_wait);
         if (active) {
-            pv_tile<DP>(vs, sacc, g, li, oacc, live);
+            if constexpr (SPLIT)
+                pv_sub<DP>(vs, ssub, g, li, oacc, wave);
+            else
+                pv_tile<DP>(vs, sacc, g, li, oacc, live);
             if constexpr (TIMED) {
                 settle(oacc);
                 lap(clk, clk->pv);
@@ -641,6 +760,54 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         }
     }
     l = sum_xor32(sum_xor16(l));
+
+    if constexpr (SPLIT) {
+        // Partial states to LDS (the K tile holds the outputs [wave][n][r][lane],
+        // the V tile the max and sum of each wave's lanes), then wave w finishes
+        // the 16-byte chunks c = w, w + 4, ... of its lane's row.
+        barrier_after_reads();
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ks[((wave * NT + n) * 4 + r) * 64 + lane] = oacc[n][r];
+        vs[wave * 64 + lane] = m;
+        vs[(kWaves + wave) * 64 + lane] = l;
+        __syncthreads();
+        float mw[kWaves], sw[kWaves];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            mw[w] = vs[w * 64 + lane];
+            mx = fmaxf(mx, mw[w]);
+        }
+        const float m_use = mx == -INFINITY ? 0.f : mx;
+        float lsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            sw[w] = fast_exp2((mw[w] - m_use) * c_exp);
+            lsum += sw[w] * vs[(kWaves + w) * 64 + lane];
+        }
+        if (qi < (packed ? valid : a.seq)) {
+            const bool zero_row = !(qi < valid && lsum > 0.f);
+            const float inv = zero_row ? 0.f : 1.f / lsum;
+            float *orow = ob + (int64_t)qi * a.o_rs + g * DQ;
+            for (int c = wave; c < DQ / 4; c += kWaves) {
+                if (g * DQ + 4 * c < D) {
+                    float e4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int n = (4 * c + e) % NT, r = (4 * c + e) / NT;
+                        float acc = 0.f;
+#pragma unroll
+                        for (int w = 0; w < kWaves; ++w) acc += sw[w] * ks[((w * NT + n) * 4 + r) * 64 + lane];
+                        e4[e] = zero_row ? 0.f : acc * inv;
+                    }
+                    *(float4 *)(orow + 4 * c) = make_float4(e4[0], e4[1], e4[2], e4[3]);
+                }
+            }
+        }
+        return;
+    }
 
     // Register r of oacc[n] holds dim g DQ + NT r + n of row qi.  Rows at or
     // beyond valid, and rows with no weight, are stored as literal zeros: their
@@ -683,17 +850,26 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel
     attend_body<DP, true, false, true>(a, p, ks, vs, nullptr);
 }
 
+// 16-row items with the key tiles split over the four waves, for grids that
+// leave most compute units idle with 64-row items.
+template <int DP, bool FUSED>
+__global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_split_kernel(const AttnLaunch a, const Plan p) {
+    __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
+    __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
+    attend_body<DP, FUSED, false, false, true>(a, p, ks, vs, nullptr);
+}
+
 // The same kernel with the stage clock.  Per-wave totals are summed in LDS,
 // then one thread per stage adds the workgroup's sum to the caller's totals.
 // An item whose rows are all padding returns from the body in every wave with
 // zero totals.
-template <int DP, bool FUSED, bool SKIP>
+template <int DP, bool FUSED, bool SKIP, bool SPLIT = false>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_timed_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
     __shared__ uint64_t part[kWaves][5];
     StageClock c{};
-    attend_body<DP, FUSED, true, SKIP>(a, p, ks, vs, &c);
+    attend_body<DP, FUSED, true, SKIP, SPLIT>(a, p, ks, vs, &c);
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
         part[wave][0] = c.qk;
@@ -719,9 +895,26 @@ int scatter_half_bits(int64_t total) {
     return h;
 }
 
+// Grids of fewer 64-row items than this take the split kernel (16-row items,
+// each tile's keys split over the waves).
+constexpr int64_t kSplitBelow = 256;
+
+// RAYA_ATTN_ITEMS=16 or 64 forces the item height (as the reference's
+// RAYA_BACKEND forces a micro-kernel backend); anything else selects by grid.
+bool use_split(const AttnLaunch &a) {
+    if (const char *e = std::getenv("RAYA_ATTN_ITEMS")) {
+        if (!std::strcmp(e, "16")) return true;
+        if (!std::strcmp(e, "64")) return false;
+    }
+    const int64_t items = (a.seq + kQRows - 1) / kQRows * a.heads * a.batch;
+    return items < kSplitBelow;
+}
+
 template <int DP, bool FUSED = false>
 hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
-    const int64_t n_qt = (a.seq + kQRows - 1) / kQRows;
+    const bool split = use_split(a);
+    const int64_t rows = split ? kSplitRows : kQRows;
+    const int64_t n_qt = (a.seq + rows - 1) / rows;
     const int64_t total = n_qt * a.heads * a.batch;
     if (total > 0x7fffffff) return hipErrorInvalidValue;
     Plan p;
@@ -735,6 +928,13 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     p.pairs_per_xcd = pairs % kXcds == 0 ? (int)(pairs / kXcds) : 0;
     const dim3 grid((unsigned)total), block(kThreads);
     const bool sliding = a.mask_kind == RAYA_MASK_SLIDING || a.mask_kind == RAYA_MASK_WINDOW64;
+    if (split) {
+        if (a.stage_cycles)
+            hipLaunchKernelGGL((attend_timed_kernel<DP, FUSED, false, true>), grid, block, 0, stream, a, p);
+        else
+            hipLaunchKernelGGL((attend_split_kernel<DP, FUSED>), grid, block, 0, stream, a, p);
+        return hipGetLastError();
+    }
     if constexpr (FUSED) {
         if (a.stage_cycles && sliding)
             hipLaunchKernelGGL((attend_timed_kernel<DP, true, true>), grid, block, 0, stream, a, p);

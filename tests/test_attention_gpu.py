@@ -19,6 +19,14 @@ from tests.conftest import GOLDEN
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True, params=["64", "16"], ids=["items64", "items16"])
+def item_rows(request, monkeypatch):
+    """Every test runs on both attention kernels: 64-row items (the large grids) and
+    16-row items with each tile's keys split over the waves (the small grids)."""
+    monkeypatch.setenv("RAYA_ATTN_ITEMS", request.param)
+    return int(request.param)
+
 MAX_ABS = 1e-5
 REL_L2 = 1e-5
 
@@ -390,3 +398,21 @@ def test_non_finite_v_outside_a_window(hip_attention):
         assert (np.isnan(gc) | same).all()
         assert np.abs(gc[same] - wc[same]).max() < MAX_ABS
         print(f"{mask.name()}: {int((~same).sum())} of {gc.size} rows outside the window are NaN in dim {c}")
+
+
+def test_scale_zero_weighs_allowed_keys_uniformly(hip_attention):
+    """A zero scale makes every allowed key weigh the same (s = 0 for all, as the reference
+    computes it); masked keys still weigh nothing."""
+    q, k, v = oracle.qkv(2, 300, 64, 5)
+    for name in ("block3", "window64", "sliding8", "block_diag64"):
+        mask, okind, block, window = MASKS[name]
+        h, s_, d = q.shape
+        out = np.full(q.shape, 7.0, np.float32)
+        hip_attention.attend(R.AttnShape(h, s_, d), R.AttnParams(mask, 128, 250, 0.0),
+                             q.ravel(), k.ravel(), v.ravel(), out.reshape(-1))
+        want = oracle.naive_attend(q, k, v, okind, 250, 0.0, block=block, window=window)
+        assert np.isfinite(out).all()
+        check_close(out, want, name)
+        i = 100
+        r = mask.key_range(i, 250)
+        assert np.abs(out[:, i] - v[:, r.start:r.stop].mean(axis=1)).max() < 1e-5

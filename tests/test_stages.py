@@ -61,22 +61,22 @@ def test_empty_shape_times_nothing():
 
 # --- on the GPU --------------------------------------------------------------------------
 
-def scheduled_tiles(mask: R.Mask, seq: int, valids, heads: int) -> int:
-    """Tiles of 16 query rows x 64 keys the kernel computes: per workgroup of 64
-    rows, the 64-key tiles spanning the rows' key ranges; per wave of 16 rows,
-    those tiles that meet the wave's keys."""
+def scheduled_tiles(mask: R.Mask, seq: int, valids, heads: int, rows: int = 64) -> int:
+    """Tiles of 16 query rows x 64 keys the kernel computes: per workgroup of `rows`
+    rows, the 64-key tiles spanning the rows' key ranges; per group of 16 rows (a wave,
+    or with 16-row items the whole workgroup), those tiles that meet the group's keys."""
     def kr(i, valid):
         r = mask.key_range(i, valid)
         return r.start, r.stop
 
     n = 0
     for valid in valids:
-        for q0 in range(0, seq, 64):
+        for q0 in range(0, seq, rows):
             if q0 >= valid:
                 continue
-            k_lo, k_hi = kr(q0, valid)[0], kr(min(q0 + 64, valid) - 1, valid)[1]
+            k_lo, k_hi = kr(q0, valid)[0], kr(min(q0 + rows, valid) - 1, valid)[1]
             for kt in range(k_lo, k_hi, 64):
-                for w in range(4):
+                for w in range(rows // 16):
                     qw = q0 + 16 * w
                     if qw >= valid:
                         continue
@@ -85,9 +85,17 @@ def scheduled_tiles(mask: R.Mask, seq: int, valids, heads: int) -> int:
     return n * heads
 
 
+@pytest.fixture(params=["64", "16"], ids=["items64", "items16"])
+def item_rows(request, monkeypatch):
+    """Both attention kernels: 64-row items, and 16-row items with each tile's keys split
+    over the waves (forced with RAYA_ATTN_ITEMS)."""
+    monkeypatch.setenv("RAYA_ATTN_ITEMS", request.param)
+    return int(request.param)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("mask", [R.Mask.WINDOW64, R.Mask.BLOCK3], ids=["window64", "block3"])
-def test_stage_percentages_sum_to_one_hundred_when_timed(hip_attention, mask):
+def test_stage_percentages_sum_to_one_hundred_when_timed(hip_attention, mask, item_rows):
     """stages.rs:7-32 on its shape (2 heads, L=512, D=64)."""
     shape = R.AttnShape(2, 512, 64)
     params = R.AttnParams.new(mask, 512, 64)
@@ -98,14 +106,14 @@ def test_stage_percentages_sum_to_one_hundred_when_timed(hip_attention, mask):
     a, b, c = times.percentages()
     assert abs(a + b + c - 100.0) < 1e-6
     assert times.qk > 0 and times.softmax > 0 and times.pv > 0 and times.load_wait > 0
-    assert times.tiles == scheduled_tiles(mask, 512, [512], 2)
+    assert times.tiles == scheduled_tiles(mask, 512, [512], 2, item_rows)
     plain = np.full(shape.numel(), 3.0, np.float32)
     hip_attention.attend(shape, params, q, k, v, plain)
     assert np.array_equal(out, plain)
 
 
 @pytest.mark.gpu
-def test_batched_stages_accumulate_and_match_the_plain_kernel(hip_attention):
+def test_batched_stages_accumulate_and_match_the_plain_kernel(hip_attention, item_rows):
     """H=12, L=2048, D=64, BlockDiag(64), padded valid lengths; two launches into one
     total (StageTimes::merge), outputs bit-identical to raya_attend_batched."""
     import torch
@@ -119,7 +127,7 @@ def test_batched_stages_accumulate_and_match_the_plain_kernel(hip_attention):
     plain = torch.empty_like(q)
     hip_attention.attend_batched(q, k, v, plain, valid, mask)
     one = hip_attention.attend_batched_stages(q, k, v, torch.empty_like(q), valid, mask)
-    assert one.tiles == scheduled_tiles(mask, s, valid_np.tolist(), h)
+    assert one.tiles == scheduled_tiles(mask, s, valid_np.tolist(), h, item_rows)
     stages = torch.zeros(5, dtype=torch.int64, device="cuda")
     timed = torch.full_like(q, 9.0)
     for _ in range(2):
