@@ -2,6 +2,7 @@
 """Throughput of raya's block-local attention hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--workload NAME] [--no-encoder]
+    python bench.py --refbench [--refbench-out PATH]
 
 A step is one launch of the fused fp32 attention kernel over one whole batch
 whose Q, K, V (seeded N(0, 1)) are already resident in HBM.  The default
@@ -11,17 +12,38 @@ line: TFLOP/s on the algorithmic FLOP count (valid rows only), the kernel's
 HBM roofline fraction (HIP events on the launch stream), and the reference's
 Tiled CPU algorithm timed on this host on the same inputs.
 
-With the default workload the line also carries "encoder": sequences/sec of the
-full 12-layer ModernBERT-base decision-model forward (B=64, L=512, valid
-lengths uniform in [128, 512], random N(0, 0.02) weights from a safetensors
-checkpoint) and the oracle's CPU forward on the first sequences beside it, and
-"encoder_layer": one block-local layer of that model on B=16 x L=1024 valid
-tokens (BlockDiag(64) on the local layers), from the forward's own per-layer
-event spans.
+Before the W warm-up steps every attention line runs its kernel back to back for
+RAMP_MS of wall time ("ramp" in the line): from idle, the first ~150 launches of
+the headline kernel run up to 25% slower while the GPU's power state rises, and
+a handful of warm-up steps would time that transition instead of the kernel.
+
+With the default workload the line also carries:
+* "workloads": the other attention configurations, each with its own roofline
+  and CPU baseline: one sequence of 12 x 512 (BlockDiag(64) and the reference's
+  Block3; also the reference's Naive on one thread), 4 x 12 x 16384 with x20
+  outliers (BlockDiag(128) and Block3), and the headline batch under Block3.
+  Launches that take a few microseconds are timed as replays of a HIP graph of
+  20 launches (the Python launch path alone takes ~8 us); their eager figure is
+  reported beside it;
+* "encoder": sequences/sec of the full 12-layer ModernBERT-base decision-model
+  forward (B=64, L=512, valid lengths uniform in [128, 512], random N(0, 0.02)
+  weights from a safetensors checkpoint) and the oracle's CPU forward on the
+  first sequences beside it;
+* "encoder_layer": one block-local layer of that model on B=16 x L=1024 valid
+  tokens (BlockDiag(64) on the local layers), from the forward's own per-layer
+  event spans;
+* "encoder_gemms": the encoder's four GEMM shapes alone.
+
+--refbench writes the reference bench's result document
+(crates/raya-kernels/benches/local_attention.rs:89-172): label, metadata and one
+row per kernel x mask x seq x threads with mean_ms, stddev_ms, samples and
+stages, for this GPU beside the Tiled restatement (1 thread and all threads) and
+Naive (1 thread) on 16 heads x L in {2048, 4096, 8192} x {Block3, Window64}.
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import statistics
@@ -31,14 +53,32 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from raya_amd.workloads import (ATTENTION as WORKLOADS, DEFAULT_ATTENTION as DEFAULT, ENCODER,  # noqa: E402
+                                ENCODER_WEIGHT_SEED, LAYER, REF_BLOCK, algorithmic, attention_inputs,
+                                encoder_inputs, mask_name)
+
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
 METRIC = "fp32 block-local attn TFLOP/s + % roofline; encoder sequences/sec, 1 GPU"
+RAMP_MS = 60.0
+GRAPH_LAUNCHES = 20
+# Launches shorter than this are timed from graph replays (eager launches are host-bound).
+GRAPH_BELOW_MS = 0.05
+# Ordered so that lines drawing the same inputs (same batch, another mask) follow each other.
+SUBLINES = ["attn_b32_h12_l2048_d64_block3",
+            "attn_b1_h12_l512_d64_blockdiag64", "attn_b1_h12_l512_d64_block3",
+            "attn_b4_h12_l16384_d64_blockdiag128", "attn_b4_h12_l16384_d64_block3"]
+_INPUTS: dict = {}
 
-from raya_amd.workloads import (ATTENTION as WORKLOADS, DEFAULT_ATTENTION as DEFAULT, ENCODER,  # noqa: E402
-                                ENCODER_WEIGHT_SEED, LAYER, REF_BLOCK, algorithmic, encoder_inputs,
-                                mask_name)
-from raya_amd.workloads import attention_inputs as make_inputs  # noqa: E402
+
+def cached_inputs(wl):
+    """attention_inputs(wl), reused by the next line that draws the same batch."""
+    key = (wl["family"], wl["batch"], wl["heads"], wl["seq"], wl["valid"], wl["outliers"], wl["data"])
+    if key not in _INPUTS:
+        _INPUTS.clear()
+        _INPUTS[key] = attention_inputs(wl)
+    return _INPUTS[key]
+NAIVE_T1 = {"attn_b1_h12_l512_d64_blockdiag64", "attn_b1_h12_l512_d64_block3"}
 
 
 def log(msg: str) -> None:
@@ -52,20 +92,127 @@ def host_cpu() -> dict:
     return meta.host_cpu()
 
 
-def cpu_baseline(qkv, valid, wl, budget_s: float):
-    """The reference's Tiled algorithm (AVX2+FMA when present) on this host's cores."""
+def cpu_threads() -> int:
+    return min(16, len(os.sched_getaffinity(0)))
+
+
+def kernel_mask(spec):
+    import raya_amd as R
+
+    return {"block_diag": lambda: R.Mask.block_diag(spec[1]), "block3": lambda: R.Mask.BLOCK3,
+            "window64": lambda: R.Mask.WINDOW64}[spec[0]]()
+
+
+def oracle_mask(spec):
     import oracle
 
-    b, h, s, d, mask = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"], wl["mask"]
     kind = {"block_diag": oracle.MASK_BLOCKDIAG, "block3": oracle.MASK_BLOCK3,
-            "window64": oracle.MASK_WINDOW64}[mask[0]]
-    block = mask[1] if mask[0] == "block_diag" else REF_BLOCK
-    threads = min(16, len(os.sched_getaffinity(0)))
+            "window64": oracle.MASK_WINDOW64}[spec[0]]
+    return kind, (spec[1] if spec[0] == "block_diag" else REF_BLOCK)
+
+
+# --- GPU timing -------------------------------------------------------------------------------
+
+def ramp(step, ms: float = RAMP_MS) -> int:
+    """Back-to-back launches for `ms` of wall time (synchronising every 20); returns the count."""
+    import torch
+
+    n, t_end = 0, time.perf_counter() + ms / 1e3
+    while time.perf_counter() < t_end:
+        for _ in range(20):
+            step()
+        n += 20
+        torch.cuda.synchronize()
+    return n
+
+
+def time_eager(step, steps: int, stream) -> tuple[float, float]:
+    """(average kernel seconds from one event pair on the launch stream around `steps`
+    back-to-back launches, host wall seconds per step)."""
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    return e0.elapsed_time(e1) / 1e3 / steps, wall
+
+
+def time_graph(launch_on, steps: int, stream) -> float:
+    """Average seconds per launch over replays of a HIP graph holding GRAPH_LAUNCHES
+    launches (captured on a side stream), one event pair around the replays."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            for _ in range(GRAPH_LAUNCHES):
+                launch_on(side)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, steps // GRAPH_LAUNCHES)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (reps * GRAPH_LAUNCHES)
+
+
+def traffic_for(workload: str) -> dict | None:
+    """HBM bytes per launch measured by the rocprofv3 counter passes committed under
+    profiles/ (not by this run), with where they came from and whether the attention
+    source they were measured on is the one built now."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    rec = json.load(open(path))
+    src = os.path.join(ROOT, "raya_amd", "csrc", "attention.hip")
+    sha = hashlib.sha256(open(src, "rb").read()).hexdigest()[:16]
+    return {"bytes": rec.get("hbm_bytes_per_launch"),
+            "source": f"profiles/{workload}_traffic.json (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)",
+            "kernel_source_sha16": rec.get("attention_source_sha16"),
+            "matches_this_build": rec.get("attention_source_sha16") == sha}
+
+
+def roofline(flops: int, nbytes: int, seconds: float, workload: str) -> dict:
+    """The bound the arithmetic intensity reaches first (ridge 157.3 TFLOP/s / 8 TB/s)."""
+    t = traffic_for(workload)
+    extra = {"traffic": t["bytes"] if t else None,
+             "traffic_source": ({k: t[k] for k in ("source", "kernel_source_sha16", "matches_this_build")}
+                                if t else None)}
+    if flops / nbytes < PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
+        achieved = nbytes / seconds / 1e9
+        return {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, **extra}
+    achieved = flops / seconds / 1e12
+    return {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / PEAK_FP32_MFMA_TFLOPS, **extra}
+
+
+# --- CPU baselines ------------------------------------------------------------------------------
+
+def cpu_tiled(qkv, valid, wl, budget_s: float):
+    """The reference's Tiled algorithm (AVX2+FMA when present) on this host's cores, whole
+    workload, median of repeated runs; plus one thread on the first sequences."""
+    import oracle
+
+    b, h, s, d = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"]
+    kind, block = oracle_mask(wl["mask"])
+    threads = cpu_threads()
     q, k, v = qkv
     backend = 1 if oracle.cpu_has_avx2_fma() else 0
-    flops, _ = algorithmic(valid, h, d, s, mask)
-    times = []
-    out = None
+    flops, _ = algorithmic(valid, h, d, s, wl["mask"])
+    times, out, used = [], None, 0
     t_end = time.perf_counter() + budget_s
     while True:
         t0 = time.perf_counter()
@@ -75,9 +222,8 @@ def cpu_baseline(qkv, valid, wl, budget_s: float):
         if time.perf_counter() > t_end or len(times) >= 50:
             break
     med = statistics.median(times)
-    # single-thread figure on the first sequences (the reference bench's t1 leg)
     n1 = max(1, min(b, 4))
-    f1, _ = algorithmic(valid[:n1], h, d, s, mask)
+    f1, _ = algorithmic(valid[:n1], h, d, s, wl["mask"])
     t0 = time.perf_counter()
     oracle.tiled_attend_batched(q[:n1], k[:n1], v[:n1], kind, valid[:n1], 0.125, block=block,
                                 threads=1, backend=backend)
@@ -94,6 +240,89 @@ def cpu_baseline(qkv, valid, wl, budget_s: float):
         "t1_sample": f"first {n1} sequences, 1 thread, {t1 * 1e3:.1f} ms",
         "host": host_cpu(),
     }
+
+
+def cpu_naive_t1(qkv, valid, wl) -> dict:
+    """The reference's Naive kernel (sequential f32, one thread) on the whole workload."""
+    import oracle
+
+    kind, block = oracle_mask(wl["mask"])
+    flops, _ = algorithmic(valid, wl["heads"], wl["head_dim"], wl["seq"], wl["mask"])
+    t0 = time.perf_counter()
+    oracle.naive_attend_batched(*qkv, kind, valid, 0.125, block=block)
+    dt = time.perf_counter() - t0
+    return {"naive_t1_value": flops / dt / 1e12,
+            "naive_t1_sample": f"whole workload, Naive restatement, 1 thread, {dt * 1e3:.1f} ms"}
+
+
+# --- one attention workload ---------------------------------------------------------------------
+
+def attention_line(name: str, steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dict:
+    """Times workload `name` on cuda:0 (and its CPU baseline); the keys of a bench line."""
+    import numpy as np
+    import torch
+
+    import raya_amd as R
+
+    wl = WORKLOADS[name]
+    b, h, s, d = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"]
+    lo, hi = wl["valid"]
+    log(f"{name}: inputs")
+    qkv, valid = cached_inputs(wl)
+    dev = torch.device("cuda:0")
+    q, k, v = (torch.from_numpy(x).to(dev) for x in qkv)
+    vl = torch.from_numpy(valid).to(dev)
+    out = torch.empty_like(q)
+    kernel = R.HipAttention()
+    mask = kernel_mask(wl["mask"])
+    stream = torch.cuda.current_stream(dev)
+    flops, nbytes = algorithmic(valid, h, d, s, wl["mask"])
+
+    def launch_on(st):
+        kernel.attend_batched(q, k, v, out, vl, mask, stream=st)
+
+    def step():
+        launch_on(stream)
+
+    log(f"{name}: ramp {RAMP_MS:.0f} ms, warmup {warmup}, timing {steps} steps")
+    ramped = ramp(step)
+    for _ in range(warmup):
+        step()
+    kern_s, wall_s = time_eager(step, steps, stream)
+    line = {
+        "config": {"workload": name, "batch": b, "heads": h, "seq": s, "head_dim": d,
+                   "mask": mask_name(wl["mask"]),
+                   "valid_len": f"uniform [{lo}, {hi}]" if lo != hi else f"{lo} (no padding)",
+                   "inputs": ("xorshift U[-1, 1], seeds 42/43/44" if wl["data"] == "xorshift"
+                              else "N(0, 1), SplitMix64 + Box-Muller"),
+                   "outliers": "1% x20" if wl["outliers"] else "none", "flop_per_step": flops,
+                   "bytes_per_step": nbytes},
+        "ramp": {"ms": RAMP_MS, "launches": ramped},
+        "ms_per_step": wall_s * 1e3,
+        "kernel_ms": kern_s * 1e3,
+        "timing": f"one event pair around {steps} back-to-back launches",
+    }
+    if kern_s * 1e3 < GRAPH_BELOW_MS:
+        g_s = time_graph(launch_on, steps, stream)
+        line["eager_kernel_ms"] = line["kernel_ms"]
+        line["kernel_ms"] = g_s * 1e3
+        line["timing"] = (f"replays of a HIP graph of {GRAPH_LAUNCHES} launches, one event pair; "
+                          f"eager launches are host-bound ({wall_s * 1e6:.1f} us of host time per launch)")
+        kern_s = g_s
+    line["kernel_tflops"] = flops / kern_s / 1e12
+    line["mfma_frac"] = line["kernel_tflops"] / PEAK_FP32_MFMA_TFLOPS
+    line["roofline"] = roofline(flops, nbytes, kern_s, name)
+    if cpu:
+        log(f"{name}: cpu baseline")
+        cpu_out, cb = cpu_tiled(qkv, valid, wl, cpu_seconds)
+        if name in NAIVE_T1:
+            cb.update(cpu_naive_t1(qkv, valid, wl))
+        got = out.cpu().numpy()
+        cb["gpu_vs_cpu_max_abs"] = max(float(np.abs(got[i, :, : valid[i]] - cpu_out[i, :, : valid[i]]).max())
+                                       for i in range(b))
+        line["cpu_baseline"] = cb
+    line["_tensors"] = (q, k, v, out, vl, mask, stream)
+    return line
 
 
 def encoder_flops(valid, d=768, inter=3072, heads=12, layers=12, global_every=3, window=64):
@@ -300,6 +529,89 @@ def encoder_cpu_baseline(ckpt, ids, valid, pos, mask, qtype, gpu_out, budget_s: 
             "gpu_vs_cpu_act_logits_max_abs": diff}
 
 
+
+# --- the reference bench's document -------------------------------------------------------------
+
+def refbench(out_path: str | None, samples: int, naive_samples: int, cpu: bool) -> dict:
+    """benches/local_attention.rs:89-172 with this GPU's rows beside the CPU rows: 16 heads,
+    D=64, L in {2048, 4096, 8192}, Block3 and Window64, xorshift inputs (seed 42); Naive on
+    one thread, Tiled on one thread and on all threads; mean and standard deviation over
+    `samples` timings (GPU: each the mean of back-to-back launches over >= 2 ms)."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import raya_amd as R
+    from raya_amd import meta
+
+    threads = cpu_threads()
+    backend = 1 if oracle.cpu_has_avx2_fma() else 0
+    backend_name = "avx2" if backend == 1 else "portable"
+    kernel = R.HipAttention()
+    rows = []
+    for seq in (2048, 4096, 8192):
+        for m in ("block3", "window64"):
+            name = f"refbench_h16_l{seq}_d64_{m}"
+            wl = WORKLOADS[name]
+            qkv, valid = attention_inputs(wl)
+            dev = torch.device("cuda:0")
+            q, k, v = (torch.from_numpy(x).to(dev) for x in qkv)
+            vl = torch.from_numpy(valid).to(dev)
+            out = torch.empty_like(q)
+            mask = kernel_mask(wl["mask"])
+            stream = torch.cuda.current_stream(dev)
+
+            def step():
+                kernel.attend_batched(q, k, v, out, vl, mask, stream=stream)
+
+            ramp(step)
+            per = max(10, int(2e-3 / max(time_eager(step, 10, stream)[0], 1e-7)))
+            ts = [time_eager(step, per, stream)[0] * 1e3 for _ in range(samples)]
+            st = kernel.attend_batched_stages(q, k, v, torch.empty_like(q), vl, mask, stream=stream)
+            pct = st.percentages()
+            base = {"mask": m, "seq": seq, "heads": 16, "head_dim": 64}
+            rows.append({"kernel": "hip", **base, "backend": "gfx950", "threads": 0,
+                         "device": torch.cuda.get_device_name(0),
+                         "mean_ms": statistics.mean(ts), "stddev_ms": statistics.stdev(ts), "samples": samples,
+                         "stages": {"qk_pct": pct[0], "softmax_pct": pct[1], "pv_pct": pct[2]}})
+            log(f"refbench {name}: gpu {rows[-1]['mean_ms']:.4f} ms")
+            if not cpu:
+                continue
+            kind, block = oracle_mask(wl["mask"])
+            cq, ck, cv = qkv
+            for t in sorted({1, threads}):
+                tt = []
+                for _ in range(samples):
+                    t0 = time.perf_counter()
+                    oracle.tiled_attend_batched(cq, ck, cv, kind, valid, 0.125, block=block, threads=t,
+                                                backend=backend)
+                    tt.append((time.perf_counter() - t0) * 1e3)
+                rows.append({"kernel": "tiled", **base, "backend": backend_name, "threads": t,
+                             "mean_ms": statistics.mean(tt), "stddev_ms": statistics.stdev(tt),
+                             "samples": samples})
+            tn = []
+            for _ in range(naive_samples):
+                t0 = time.perf_counter()
+                oracle.naive_attend(cq[0], ck[0], cv[0], kind, int(valid[0]), 0.125, block=block)
+                tn.append((time.perf_counter() - t0) * 1e3)
+            rows.append({"kernel": "naive", **base, "backend": "scalar", "threads": 1,
+                         "mean_ms": statistics.mean(tn),
+                         "stddev_ms": statistics.stdev(tn) if len(tn) > 1 else 0.0, "samples": naive_samples})
+            log(f"refbench {name}: cpu rows done")
+            del q, k, v, out
+            torch.cuda.empty_cache()
+    md = meta.collect(threads=threads)
+    md["backend"] = backend_name if cpu else md["backend"]
+    doc = {"label": md["label"], "metadata": md, "results": rows}
+    if out_path is None:
+        out_path = os.path.join("results", "kernel-bench", md["timestamp"].replace(":", "-") + ".json")
+    os.makedirs(os.path.dirname(os.path.abspath(out_path)), exist_ok=True)
+    with open(out_path, "w") as f:
+        json.dump(doc, f, indent=1)
+    log(f"wrote {out_path}")
+    return doc
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -309,20 +621,31 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-encoder", action="store_true", help="skip the encoder forward leg")
+    ap.add_argument("--no-sublines", action="store_true", help="skip the other attention workloads")
     ap.add_argument("--encoder-steps", type=int, default=10)
     ap.add_argument("--encoder-warmup", type=int, default=2)
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only the encoder's four GEMM shapes and print their line")
+    ap.add_argument("--refbench", action="store_true",
+                    help="write the reference bench's result document instead of the bench line")
+    ap.add_argument("--refbench-out", default=None)
+    ap.add_argument("--refbench-samples", type=int, default=10)
+    ap.add_argument("--refbench-naive-samples", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
               file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
-    import raya_amd as R
+    if args.refbench:
+        doc = refbench(args.refbench_out, args.refbench_samples, args.refbench_naive_samples,
+                       cpu=not args.no_cpu_baseline)
+        print(json.dumps({"refbench_rows": len(doc["results"]), "label": doc["label"],
+                          "gpu_rows": [{k: r[k] for k in ("mask", "seq", "mean_ms", "stddev_ms")}
+                                       for r in doc["results"] if r["kernel"] == "hip"]}), flush=True)
+        return 0
 
     if args.gemm_only:
         gm = bench_gemms(args.steps, args.warmup)
@@ -336,87 +659,31 @@ def main() -> int:
                           "gemms": gm}), flush=True)
         return 0
 
-    wl = WORKLOADS[args.workload]
-    b, h, s, d, mask_spec = wl["batch"], wl["heads"], wl["seq"], wl["head_dim"], wl["mask"]
-    lo, hi = wl["valid"]
-    log(f"generating inputs for {args.workload}")
-    qkv, valid = make_inputs(wl)
-    dev = torch.device("cuda:0")
-    q, k, v = (torch.from_numpy(x).to(dev) for x in qkv)
-    vl = torch.from_numpy(valid).to(dev)
-    out = torch.empty_like(q)
-    kernel = R.HipAttention()
-    mask = {"block_diag": lambda: R.Mask.block_diag(mask_spec[1]), "block3": lambda: R.Mask.BLOCK3,
-            "window64": lambda: R.Mask.WINDOW64}[mask_spec[0]]()
-    stream = torch.cuda.current_stream(dev)
-    flops, nbytes = algorithmic(valid, h, d, s, mask_spec)
-
-    def step():
-        kernel.attend_batched(q, k, v, out, vl, mask, stream=stream)
-
-    log(f"warmup {args.warmup}")
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # One event pair on the launch stream brackets the K back-to-back launches
-    # (an event between launches costs ~10 us of idle queue per step), so the
-    # average launch duration is the bracketed time over K.
-    log(f"timing {args.steps} steps")
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        step()
-    end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    avg_kernel_s = start.elapsed_time(end) / 1e3 / args.steps
-    ms_per_step = wall / args.steps * 1e3
-
+    head = attention_line(args.workload, args.steps, args.warmup, args.cpu_seconds,
+                          cpu=not args.no_cpu_baseline)
+    q, k, v, out, vl, mask, stream = head.pop("_tensors")
+    flops = head["config"]["flop_per_step"]
     result = {
         "metric": METRIC,
-        "value": flops / (ms_per_step / 1e3) / 1e12,
+        "value": flops / (head["ms_per_step"] / 1e3) / 1e12,
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms_per_step,
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": args.workload, "batch": b, "heads": h, "seq": s, "head_dim": d,
-                   "mask": mask_name(mask_spec),
-                   "valid_len": f"uniform [{lo}, {hi}]" if lo != hi else f"{lo} (no padding)",
-                   "inputs": ("xorshift U[-1, 1], seeds 42/43/44" if wl["data"] == "xorshift"
-                              else "N(0, 1), SplitMix64 + Box-Muller"),
-                   "outliers": "1% x20" if wl["outliers"] else "none", "flop_per_step": flops,
-                   "bytes_per_step": nbytes},
-        "kernel_ms": avg_kernel_s * 1e3,
-        "kernel_tflops": flops / avg_kernel_s / 1e12,
-        "mfma_frac": flops / avg_kernel_s / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+        **{key: head[key] for key in head if key not in ("ms_per_step",)},
     }
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"{args.workload}_traffic.json")
-    if os.path.exists(tpath):
-        traffic = json.load(open(tpath)).get("hbm_bytes_per_launch")
-    # The bound is the one the arithmetic intensity reaches first.
-    if flops / nbytes < PEAK_FP32_MFMA_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9):
-        achieved = nbytes / avg_kernel_s / 1e9
-        result["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS,
-                              "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": traffic}
-    else:
-        achieved = flops / avg_kernel_s / 1e12
-        result["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS,
-                              "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
-                              "traffic": traffic}
 
     # One launch of the instrumented kernel after the timed region: where the
     # waves' cycles go (the reference's stage-timing split, tiled/stages.rs).
-    st = kernel.attend_batched_stages(q, k, v, out, vl, mask, stream=stream)
+    import raya_amd as R
+
+    st = R.HipAttention().attend_batched_stages(q, k, v, out, vl, mask, stream=stream)
     pct = st.percentages()
     waves = st.qk + st.softmax + st.pv + st.load_wait
     result["stage_split"] = {
@@ -424,23 +691,24 @@ def main() -> int:
         "load_wait_of_wave_cycles_pct": 100.0 * st.load_wait / waves, "tiles": st.tiles,
         "source": "one instrumented launch after the timed region; shares of per-wave shader "
                   "clock cycles (qk/softmax/pv as in the reference's StageTimes::percentages)"}
+    del q, k, v, out
+    torch.cuda.empty_cache()
 
     # BenchMetadata (crates/raya-kernels/src/meta.rs): host, GPU and build; threads is
     # the CPU baseline's worker count.
     from raya_amd import meta
 
-    result["meta"] = meta.collect(threads=0 if args.no_cpu_baseline
-                                  else min(16, len(os.sched_getaffinity(0))))
+    result["meta"] = meta.collect(threads=0 if args.no_cpu_baseline else cpu_threads())
 
-    if not args.no_cpu_baseline:
-        log("cpu baseline")
-        cpu_out, cb = cpu_baseline(qkv, valid, wl, args.cpu_seconds)
-        got = out.cpu().numpy()
-        diff = 0.0
-        for i in range(b):
-            diff = max(diff, float(np.abs(got[i, :, : valid[i]] - cpu_out[i, :, : valid[i]]).max()))
-        cb["gpu_vs_cpu_max_abs"] = diff
-        result["cpu_baseline"] = cb
+    if args.workload == DEFAULT and not args.no_sublines:
+        subs = {}
+        for name in SUBLINES:
+            line = attention_line(name, args.steps, args.warmup, min(args.cpu_seconds, 2.0),
+                                  cpu=not args.no_cpu_baseline)
+            line.pop("_tensors")
+            subs[name] = line
+            torch.cuda.empty_cache()
+        result["workloads"] = subs
     if args.workload == DEFAULT and not args.no_encoder:
         enc = bench_encoder(args.encoder_steps, args.encoder_warmup, args.cpu_seconds,
                             cpu=not args.no_cpu_baseline)
