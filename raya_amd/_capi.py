@@ -134,6 +134,14 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(LIB_PATH):
             raise ImportError(
                 f"{LIB_PATH} is missing: build the HIP backend with `python -m raya_amd.build`")
+        # torch ships its own HIP and HSA runtimes.  Loaded first, its HSA runtime
+        # (soname libhsa-runtime64.so.1) also serves this library's HIP runtime; loaded
+        # after this library, torch brings a second HSA runtime into the process and
+        # whichever HIP runtime initialises second finds no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         for name, res, args in SIGNATURES:
             f = getattr(L, name)
