@@ -13,6 +13,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libraya_hip
 RAYA_OK, RAYA_ERR_SHAPE, RAYA_ERR_LENGTH, RAYA_ERR_UNSUPPORTED, RAYA_ERR_DEVICE = 0, 1, 2, 3, 4
 RAYA_MASK_BLOCK3, RAYA_MASK_WINDOW64, RAYA_MASK_FULL, RAYA_MASK_SLIDING, RAYA_MASK_BLOCKDIAG = range(5)
 RAYA_BLOCK, RAYA_WINDOW = 128, 64
+RAYA_STATIC_ATTEND_MAX_NUMEL = 4194304
 RAYA_EPI_NONE, RAYA_EPI_GELU, RAYA_EPI_RELU, RAYA_EPI_GEGLU = 0, 1, 2, 3
 RAYA_ERR_CONFIG, RAYA_ERR_UNIMPLEMENTED, RAYA_ERR_INPUT, RAYA_ERR_KERNEL, RAYA_ERR_WEIGHTS = 5, 6, 7, 8, 9
 
@@ -103,6 +104,8 @@ SIGNATURES = [
     ("raya_build_info", ctypes.c_char_p, []),
     ("raya_attend", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
                                    _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz]),
+    ("raya_attend_static", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
+                                          _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
     ("raya_attend_with_stages", ctypes.c_int, [ctypes.POINTER(AttnShapeC), ctypes.POINTER(AttnParamsC),
                                                _vp, _sz, _vp, _sz, _vp, _sz, _vp, _sz,
                                                ctypes.POINTER(StageCyclesC)]),

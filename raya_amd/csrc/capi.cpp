@@ -129,16 +129,45 @@ int workspace(size_t bytes, void **ptr, hipStream_t *stream) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// The allocation-free host-slice entry point's staging area: four slots of
+// RAYA_STATIC_ATTEND_MAX_NUMEL floats (q, k, v, out; 64 MiB in all) that each
+// device holds from the library's load until the process ends.  Host code never
+// uses the array's name as an address (on the host it is a stand-in symbol):
+// the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kStaticSlotFloats = RAYA_STATIC_ATTEND_MAX_NUMEL;
+static __device__ __align__(256) float scratch[4 * kStaticSlotFloats];
+
+std::mutex g_static_mutex;  // held for a whole call: calls on any device run one at a time
+std::unordered_map<int, float *> g_static_ptr;
+
+int static_scratch(float **ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail_device(e, "hipGetDevice");
+    auto it = g_static_ptr.find(dev);
+    if (it == g_static_ptr.end()) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) return fail_device(e, "hipGetSymbolAddress(scratch)");
+        it = g_static_ptr.emplace(dev, (float *)p).first;
+    }
+    *ptr = it->second;
+    return RAYA_OK;
+}
+
 }  // namespace
 }  // namespace raya
 
 using namespace raya;
 
 // raya_attend, and with `stages` (host) set raya_attend_with_stages: the
-// device totals live in a 256-byte slot after the four operand slots.
+// device totals live in a 256-byte slot after the four operand slots.  With
+// `fixed` set, raya_attend_static: the operands are staged in the static
+// scratch array instead of the grow-only workspace, on the caller's stream.
 static int attend_host(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
                        size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
-                       float *out, size_t out_len, raya_stage_cycles *stages) {
+                       float *out, size_t out_len, raya_stage_cycles *stages, bool fixed = false,
+                       void *user_stream = nullptr) {
     if (!shape || !params) return fail(RAYA_ERR_SHAPE, "invalid shape: null shape or params");
     int rc = check_attn(shape->heads, shape->head_dim, shape->seq, params->block, &params->valid_len);
     if (rc) return rc;
@@ -155,17 +184,30 @@ static int attend_host(const raya_attn_shape *shape, const raya_attn_params *par
         if (bf.len != numel) return fail_length(bf.name, bf.len, numel);
     rc = check_hip_limits(shape->heads, shape->seq, shape->head_dim, params->mask_kind, params->mask_arg);
     if (rc) return rc;
+    if (fixed && numel > kStaticSlotFloats)
+        return fail(RAYA_ERR_UNSUPPORTED,
+                    "unsupported: heads x seq x head_dim = %" PRIu64 " exceeds the static workspace (%d floats per buffer)",
+                    numel, RAYA_STATIC_ATTEND_MAX_NUMEL);
     if (stages) *stages = raya_stage_cycles{};
     if (numel == 0) return ok();
     if (!q || !k || !v || !out) return fail(RAYA_ERR_SHAPE, "invalid shape: null buffer");
 
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    std::lock_guard<std::mutex> lock(fixed ? g_static_mutex : g_ws_mutex);
     void *base = nullptr;
     hipStream_t stream = nullptr;
     const size_t bytes = numel * sizeof(float);
-    const size_t slot = (bytes + 255) / 256 * 256;
-    rc = workspace(4 * slot + (stages ? 256 : 0), &base, &stream);
-    if (rc) return rc;
+    size_t slot = (bytes + 255) / 256 * 256;
+    if (fixed) {
+        float *sp = nullptr;
+        rc = static_scratch(&sp);
+        if (rc) return rc;
+        base = sp;
+        slot = kStaticSlotFloats * sizeof(float);
+        stream = (hipStream_t)user_stream;
+    } else {
+        rc = workspace(4 * slot + (stages ? 256 : 0), &base, &stream);
+        if (rc) return rc;
+    }
     char *p = (char *)base;
     float *dq = (float *)p, *dk = (float *)(p + slot), *dv = (float *)(p + 2 * slot),
           *dout = (float *)(p + 3 * slot);
@@ -234,6 +276,12 @@ int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params, co
                 size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len,
                 float *out, size_t out_len) {
     return attend_host(shape, params, q, q_len, k, k_len, v, v_len, out, out_len, nullptr);
+}
+
+int raya_attend_static(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
+                       size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len, float *out,
+                       size_t out_len, void *stream) {
+    return attend_host(shape, params, q, q_len, k, k_len, v, v_len, out, out_len, nullptr, true, stream);
 }
 
 int raya_attend_with_stages(const raya_attn_shape *shape, const raya_attn_params *params,

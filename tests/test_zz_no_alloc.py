@@ -1,0 +1,88 @@
+"""raya_attend_static: raya_attend (AttentionKernel::attend on host slices, attention.rs:113-125)
+with its device staging in the library's static array instead of allocated memory.
+
+CPU: the size limit and the reference's errors come back before any GPU work.
+GPU: two calls in a row, the second on a smaller input, each equal to raya_attend's output bit
+for bit and within the oracle's bar (max-abs and rel-L2 1e-5 against Naive); the device's free
+memory does not move across the calls."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import raya_amd as R
+from raya_amd import _capi as C
+
+
+def _args(shape, params):
+    s = C.AttnShapeC(shape.heads, shape.seq, shape.head_dim)
+    p = C.AttnParamsC(params.mask.kind, params.scale, params.mask.arg, params.block, params.valid_len)
+    return s, p
+
+
+def call_static(shape, params, q, k, v, out, stream=None):
+    s, p = _args(shape, params)
+    ptr = lambda x: ctypes.c_void_p(x.ctypes.data)  # noqa: E731
+    return C.lib().raya_attend_static(ctypes.byref(s), ctypes.byref(p), ptr(q), q.size, ptr(k), k.size,
+                                      ptr(v), v.size, ptr(out), out.size, stream)
+
+
+def test_static_entry_point_checks_before_any_gpu_work():
+    """Lengths in validate()'s order first, then the static array's limit."""
+    shape = R.AttnShape(1, 4, 8)
+    params = R.AttnParams.new(R.Mask.BLOCK3, 4, 8)
+    ok = np.zeros(32, np.float32)
+    assert call_static(shape, params, ok[:3], ok, ok, ok.copy()) == C.RAYA_ERR_LENGTH
+    assert C.last_error().message.decode() == "buffer `q` has length 3, expected 32"
+    big = R.AttnShape(16, 8192, 64)  # 8,388,608 floats: twice the static slot
+    buf = np.zeros(1, np.float32)
+    s, p = _args(big, R.AttnParams.new(R.Mask.BLOCK3, 8192, 64))
+    n = big.numel()
+    rc = C.lib().raya_attend_static(ctypes.byref(s), ctypes.byref(p), ctypes.c_void_p(buf.ctypes.data), n,
+                                    ctypes.c_void_p(buf.ctypes.data), n, ctypes.c_void_p(buf.ctypes.data), n,
+                                    ctypes.c_void_p(buf.ctypes.data), n, None)
+    assert rc == C.RAYA_ERR_UNSUPPORTED
+    assert "static workspace" in C.last_error().message.decode()
+    assert n > C.RAYA_STATIC_ATTEND_MAX_NUMEL
+
+
+CASES = [
+    # (heads, seq, head_dim, mask, oracle kind, block, window, valid, seed)
+    (12, 512, 64, R.Mask.BLOCK3, oracle.MASK_BLOCK3, 128, 0, 500, 1),
+    (2, 130, 64, R.Mask.WINDOW64, oracle.MASK_WINDOW64, 128, 0, 100, 2),
+]
+
+
+@pytest.mark.gpu
+def test_two_calls_match_raya_attend_without_allocating():
+    """The reference outputs come first (raya_attend grows its own workspace), then two static
+    calls in a row.  The first static call may load the code object that holds the static
+    array; across the second the device's free memory stays put."""
+    import torch
+
+    assert torch.cuda.is_available(), "needs a GPU"
+    kernel = R.HipAttention()
+    inputs, wants = [], []
+    for h, s, d, mask, kind, block, window, valid, seed in CASES:
+        q, k, v = oracle.qkv(h, s, d, seed)
+        shape, params = R.AttnShape(h, s, d), R.AttnParams.new(mask, valid, d)
+        want = np.full(q.size, 7.0, np.float32)
+        kernel.attend(shape, params, q.ravel(), k.ravel(), v.ravel(), want)
+        inputs.append((q, k, v, shape, params))
+        wants.append(want)
+    torch.cuda.synchronize()
+    free = []
+    for (h, s, d, mask, kind, block, window, valid, seed), (q, k, v, shape, params), want in zip(CASES, inputs, wants):
+        print(f"static attend: H={h} L={s} D={d} {mask.name()} valid {valid}", flush=True)
+        got = np.full(q.size, np.nan, np.float32)
+        rc = call_static(shape, params, q.ravel(), k.ravel(), v.ravel(), got)
+        assert rc == C.RAYA_OK, C.last_error().message.decode()
+        free.append(torch.cuda.mem_get_info()[0])
+        assert np.array_equal(got, want)
+        naive = oracle.naive_attend(q, k, v, kind, valid, params.scale, block=block, window=window)
+        diff = np.abs(got.reshape(q.shape).astype(np.float64) - naive)
+        rel = np.sqrt((diff ** 2).sum() / (naive.astype(np.float64) ** 2).sum())
+        assert diff.max() < 1e-5 and rel < 1e-5, (diff.max(), rel)
+        assert (got.reshape(q.shape)[:, valid:] == 0).all()
+    assert free[1] >= free[0] - (2 << 20), free
