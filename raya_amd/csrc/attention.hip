@@ -71,6 +71,7 @@ struct Plan {
     int total, half_bits, n_qt;
     FastDiv by_qt, by_heads, by_arg;  // by_arg: the BlockDiag width (1 otherwise)
     int pairs_per_xcd;                 // > 0: whole (sequence, head) pairs per XCD
+    int quads;                         // split kernel: each 4 consecutive items on one XCD
 };
 
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroup i runs on XCD i mod 8
@@ -177,11 +178,20 @@ __device__ __forceinline__ int scatter(int i, int total, int half_bits);
 // Block3 and Sliding hit in that XCD's L2), while the heads of each sequence,
 // and with them its padding, spread over all XCDs.  Otherwise a scattered
 // order.
+//
+// The split kernel's items are 16-row tiles: when the pairs do not divide
+// among the XCDs, every four consecutive items (the 16-row tiles of one 64-row
+// block, which share their key tiles) still go to one XCD, so that block's K/V
+// is fetched into one L2 once rather than into four.
 __device__ __forceinline__ int item_of(int bid, const Plan &p) {
     if (p.pairs_per_xcd > 0) {
         const int x = bid % kXcds, j = bid / kXcds;
         const int pj = fdiv(j, p.by_qt);
         return (pj * kXcds + x) * p.n_qt + (j - pj * p.n_qt);
+    }
+    if (p.quads) {  // total is a multiple of 4 * kXcds
+        const int x = bid % kXcds, j = bid / kXcds;
+        return ((j >> 2) * kXcds + x) * 4 + (j & 3);
     }
     return scatter(bid, p.total, p.half_bits);
 }
@@ -926,6 +936,7 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     p.by_arg = make_fastdiv(a.mask_kind == RAYA_MASK_BLOCKDIAG ? (uint32_t)a.mask_arg : 1u);
     const int64_t pairs = (int64_t)a.heads * a.batch;
     p.pairs_per_xcd = pairs % kXcds == 0 ? (int)(pairs / kXcds) : 0;
+    p.quads = split && p.pairs_per_xcd == 0 && total % (4 * kXcds) == 0;
     const dim3 grid((unsigned)total), block(kThreads);
     const bool sliding = a.mask_kind == RAYA_MASK_SLIDING || a.mask_kind == RAYA_MASK_WINDOW64;
     if (split) {
