@@ -209,6 +209,37 @@ unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per)
 
 }  // namespace
 
+namespace {
+
+// The pre-LN LayerNorm statistics of each row from its 64-column chunk (mean, M2)
+// pairs (Chan et al.'s pairwise combination, in f64, as ops::layer_norm keeps its
+// statistics in f64): (mean, 1 / sqrt(var + eps)), var the biased variance.
+__global__ void ln_stats_kernel(const float2 *chunks_in, int rows, int chunks, float eps, float2 *out) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const float2 *st = chunks_in + (int64_t)row * chunks;
+    double mean = 0.0;
+    for (int c = 0; c < chunks; ++c) mean += st[c].x;
+    mean /= chunks;
+    double m2 = 0.0;
+    for (int c = 0; c < chunks; ++c) {
+        const double dm = (double)st[c].x - mean;
+        m2 += (double)st[c].y + 64.0 * dm * dm;
+    }
+    const double var = m2 / (64.0 * chunks);
+    out[row] = make_float2((float)mean, (float)(1.0 / sqrt(var + (double)eps)));
+}
+
+}  // namespace
+
+hipError_t launch_ln_stats(const float2 *chunks, int rows, int n_chunks, float eps, float2 *out, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(ln_stats_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, chunks, rows,
+                       n_chunks, eps, out);
+    return hipGetLastError();
+}
+
+
 hipError_t launch_layer_norm(const LayerNormLaunch &l, hipStream_t stream) {
     if (l.rows == 0) return hipSuccess;
     const auto aligned = [](const void *p) { return ((uintptr_t)p & 15) == 0; };

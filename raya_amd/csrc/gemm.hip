@@ -259,6 +259,22 @@ __device__ __forceinline__ void dma16(const float *src, uint32_t lds_addr) {
 
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
+// Sum over each 16-lane row of the wave with DPP moves (no LDS crossbar): lane
+// pairs (quad_perm [1,0,3,2]), quads ([2,3,0,1]), then the row's four quads by
+// rotating it 4 and 8 lanes.  Lanes of a row may differ in the last bit (their
+// quad sums are added in different orders).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    x += dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    x += dpp<0x124>(x);  // row_ror 4
+    x += dpp<0x128>(x);  // row_ror 8
+    return x;
+}
+
 // Epilogue through LDS, for out (and residual) with row strides a multiple of 4
 // floats and 16-byte aligned bases.  Bias, activation, GeGLU and RoPE are
 // applied in the accumulator layout, as in epilogue(); each wave then writes
@@ -271,14 +287,30 @@ constexpr int kStageStride = 72;      // 64 columns per wave
 constexpr int kStageStrideGlu = 40;   // 32 GeGLU output columns per wave
 constexpr int kStageFloats = 32 * kStageStride;  // per wave: 32 rows at a time
 
-template <int ACT, bool ROPE>
-__device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, const floatx16 (&acc)[2][2], int m0, int n0,
-                                                int wm, int wn, int li, int h, int lane, float *stg) {
+//
+// With g.in_stats, rowstat holds (mean, rstd) of the workgroup's 128 input rows
+// and the accumulators are normalised first (see GemmLaunch).  With
+// g.out_stats, each wave's 64 output columns are one chunk: the 16 lanes that
+// hold a row reduce its sum, then its squared deviations from the chunk mean.
+template <int ACT, bool ROPE, bool NORM, bool STATS>
+__device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&acc)[2][2], int m0, int n0,
+                                                int wm, int wn, int li, int h, int lane, float *stg,
+                                                const float2 *rowstat, const float (&cs)[2]) {
     constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
     constexpr int COLS = GEGLU ? 32 : 64;  // output columns of this wave
     constexpr int S = GEGLU ? kStageStrideGlu : kStageStride;
     constexpr int C4 = COLS / 4;           // float4 per staged row
     const int c0 = n0 + (GEGLU ? (wn >> 1) : wn);  // first output column of this wave
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float2 st = rowstat[wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3)];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j][r] = st.y * (acc[i][j][r] - st.x * cs[j]);
+            }
+    }
     float bias[2] = {0.f, 0.f};
     if (g.bias) {
         if constexpr (GEGLU) {
@@ -326,31 +358,45 @@ __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, const float
         for (int t = 0; t < 32 * C4 / 64; ++t) {
             const int idx = t * 64 + lane, rr = idx / C4, c4 = idx % C4;
             const int row = m0 + wm + 32 * i + rr, col = c0 + 4 * c4;
-            if (row >= g.m || col >= g.n) continue;
-            float4 v = *(const float4 *)&stg[rr * S + 4 * c4];
-            float *o = g.out + (int64_t)row * g.ldo + col;
-            const float *res = g.residual ? g.residual + (int64_t)row * g.ldr + col : nullptr;
-            if (col + 4 <= g.n) {
-                if (res) {
-                    const float4 x = *(const float4 *)res;
-                    v.x += x.x;
-                    v.y += x.y;
-                    v.z += x.z;
-                    v.w += x.w;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (row < g.m && col < g.n) {
+                v = *(const float4 *)&stg[rr * S + 4 * c4];
+                float *o = g.out + (int64_t)row * g.ldo + col;
+                const float *res = g.residual ? g.residual + (int64_t)row * g.ldr + col : nullptr;
+                if (col + 4 <= g.n) {
+                    if (res) {
+                        const float4 x = *(const float4 *)res;
+                        v.x += x.x;
+                        v.y += x.y;
+                        v.z += x.z;
+                        v.w += x.w;
+                    }
+                    *(float4 *)o = v;
+                } else {
+                    const float e[4] = {v.x, v.y, v.z, v.w};
+                    for (int q = 0; q < 4 && col + q < g.n; ++q) o[q] = res ? e[q] + res[q] : e[q];
                 }
-                *(float4 *)o = v;
-            } else {
-                const float e[4] = {v.x, v.y, v.z, v.w};
-                for (int q = 0; q < 4 && col + q < g.n; ++q) o[q] = res ? e[q] + res[q] : e[q];
+            }
+            if constexpr (STATS && !GEGLU) {
+                // n is a multiple of 64, so this wave's 64 columns are either all in range
+                // (a chunk of the row) or all past n (a tile wider than the matrix: no chunk).
+                if (c0 < g.n) {
+                    const float mean = row16_sum((v.x + v.y) + (v.z + v.w)) * (1.0f / 64.0f);
+                    const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
+                    const float m2 = row16_sum((dx * dx + dy * dy) + (dz * dz + dw * dw));
+                    if (c4 == 0 && row < g.m) g.out_stats[(int64_t)row * (g.n / 64) + (c0 >> 6)] = make_float2(mean, m2);
+                }
             }
         }
     }
 }
 
-template <int ACT, bool ROPE>
+// NORM: the input rows' LayerNorm is folded in (GemmLaunch::in_stats); STATS:
+// the output rows' chunk statistics are written (GemmLaunch::out_stats).
+template <int ACT, bool ROPE, bool NORM = false, bool STATS = false>
 __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch g) {
     __shared__ __attribute__((aligned(16))) float ring[RSTAGES * 2 * kTileFloats];  // 48 KB
-    static_assert(4 * kStageFloats <= RSTAGES * 2 * kTileFloats, "epilogue staging fits the ring");
+    static_assert(4 * kStageFloats + 2 * BM <= RSTAGES * 2 * kTileFloats, "epilogue staging and row statistics fit the ring");
 
     constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
     constexpr int OUT_BN = GEGLU ? BN / 2 : BN;
@@ -366,6 +412,24 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
 
     // This thread's DMA sources: slot q = (2 wave + j) 64 + lane holds stored
     // chunk q % 4 of tile row q / 4, i.e. data chunk (q % 4) ^ rswz(row).
+    // The input rows' (mean, rstd), one row per thread of the first half, loaded
+    // before the K loop and used after it.
+    // The weight rows' sums this lane's columns need (GemmLaunch::colsum), likewise.
+    float2 my_rowstat = make_float2(0.f, 0.f);
+    float cs[2] = {0.f, 0.f};
+    if constexpr (NORM) {
+        if (tid < BM) my_rowstat = g.in_stats[min(m0 + tid, g.m - 1)];
+        const int c0 = n0 + (GEGLU ? (wn >> 1) : wn);
+        if constexpr (GEGLU) {
+            const int col = min(c0 + li, g.n - 1);
+            cs[0] = g.colsum[col];
+            cs[1] = g.colsum[g.n + col];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) cs[j] = g.colsum[min(c0 + 32 * j + li, g.n - 1)];
+        }
+    }
+
     const float *asrc[2], *bsrc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -445,7 +509,13 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
                          (!g.residual || ((g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15) == 0));
     if (vec_out) {
         __syncthreads();  // every wave's reads of the last slab are done: the ring is free
-        epilogue_staged<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h, lane, ring + wave * kStageFloats);
+        float2 *rowstat = (float2 *)(ring + 4 * kStageFloats);
+        if constexpr (NORM) {
+            if (tid < BM) rowstat[tid] = my_rowstat;
+            __syncthreads();
+        }
+        epilogue_staged<ACT, ROPE, NORM, STATS>(g, acc, m0, n0, wm, wn, li, h, lane, ring + wave * kStageFloats,
+                                                rowstat, cs);
     } else {
         epilogue<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h);
     }
@@ -460,16 +530,36 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
                      (((uintptr_t)g.b & 15) == 0) && (g.k % 4 == 0);
     const dim3 grid((unsigned)tiles), block(kThreads);
     const bool ring_ok = vec && g.k % RBK == 0 && g.k > 0;
+    if (g.in_stats || g.out_stats) {
+        // Only the ring kernel's staged epilogue carries them (see GemmLaunch).
+        const bool vec_out = (g.ldo & 3) == 0 && ((uintptr_t)g.out & 15) == 0 &&
+                             (!g.residual || ((g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15) == 0));
+        if (!ring_ok || !vec_out) return hipErrorInvalidValue;
+        if (g.in_stats && !g.colsum) return hipErrorInvalidValue;
+        if (g.out_stats && (ACT == RAYA_EPI_GEGLU || g.n % 64 != 0)) return hipErrorInvalidValue;
+    }
     if constexpr (ACT == RAYA_EPI_NONE) {
         if (g.rope_cos && (g.rope_cols % kRopeHeadDim != 0 || g.rope_cols > g.n)) return hipErrorInvalidValue;
     } else if (g.rope_cos) {
         return hipErrorInvalidValue;
     }
     if (ring_ok) {
-        if (g.rope_cos)
-            hipLaunchKernelGGL((gemm_ring_kernel<ACT, ACT == RAYA_EPI_NONE>), grid, block, 0, stream, g);
-        else
+        constexpr bool NONE = ACT == RAYA_EPI_NONE;
+        if (g.in_stats) {  // folded LayerNorm: QKV (with or without RoPE) and GeGLU
+            if (g.rope_cos)
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE, true>), grid, block, 0, stream, g);
+            else
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, true>), grid, block, 0, stream, g);
+        } else if (g.out_stats) {  // the residual GEMMs
+            if constexpr (NONE)
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, false, true>), grid, block, 0, stream, g);
+            else
+                return hipErrorInvalidValue;
+        } else if (g.rope_cos) {
+            hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE>), grid, block, 0, stream, g);
+        } else {
             hipLaunchKernelGGL((gemm_ring_kernel<ACT, false>), grid, block, 0, stream, g);
+        }
         return hipGetLastError();
     }
     if constexpr (ACT == RAYA_EPI_NONE) {

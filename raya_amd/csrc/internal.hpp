@@ -58,6 +58,17 @@ struct GemmLaunch {
     const float *rope_cos, *rope_sin;
     const int32_t *positions;
     int32_t rope_cols;
+    // A pre-LN LayerNorm of the input rows folded into the product (the ring
+    // kernel's staged epilogue only): b holds the weight with the norm's gain
+    // folded into its columns, colsum[j] = sum_t b[j][t], and in_stats each row's
+    // (mean, 1 / sqrt(var + eps)) ([m], from launch_ln_stats); then
+    //   y = rstd(row) * (acc - mean(row) * colsum[j])
+    // before bias, activation and RoPE, which is LayerNorm(a) @ W^T.  Null: off.
+    const float2 *in_stats;
+    const float *colsum;
+    // (mean, M2) of each output row over each 64-column chunk, after the
+    // residual add ([m][n / 64]); n a multiple of 64.  Null: off.
+    float2 *out_stats;
 };
 
 // Head dim of the fused RoPE epilogue (other head dims use launch_rope).
@@ -83,6 +94,9 @@ struct LayerNormLaunch {
 };
 
 hipError_t launch_layer_norm(const LayerNormLaunch &l, hipStream_t stream);
+// Each row's (mean, 1 / sqrt(var + eps)) from its 64-column chunk statistics
+// (GemmLaunch::out_stats, [rows][n_chunks]) into out ([rows]).
+hipError_t launch_ln_stats(const float2 *chunks, int rows, int n_chunks, float eps, float2 *out, hipStream_t stream);
 hipError_t launch_rope(float *qkv, int64_t ld, const int32_t *positions, const float *cos_t,
                        const float *sin_t, int rows, int d, int head_dim, hipStream_t stream);
 hipError_t launch_gather_rows(const float *h, int64_t ldh, const int32_t *rows, int n, int d,

@@ -15,6 +15,7 @@
 #include <cinttypes>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -538,6 +539,9 @@ int load_weights(const std::string &path, const Config &c, Weights &w) {
 struct DeviceBuf {
     void *ptr = nullptr;
     size_t bytes = 0;
+    DeviceBuf() = default;
+    DeviceBuf(const DeviceBuf &) = delete;  // one owner per allocation
+    DeviceBuf &operator=(const DeviceBuf &) = delete;
     ~DeviceBuf() {
         if (ptr) (void)hipFree(ptr);
     }
@@ -572,12 +576,21 @@ void rope_table(float theta, int head_dim, int positions, std::vector<float> &co
         }
 }
 
+// The encoder's pre-LN LayerNorms folded into the GEMMs that read them (GemmLaunch::in_stats):
+// per layer, Wqkv (layers >= 1, after attn_norm) and Wi (after mlp_norm) with the norm's gain
+// multiplied into their columns, and each weight row's sum.  Offsets in floats into `buf`.
+struct FoldedNorms {
+    DeviceBuf buf;
+    std::vector<size_t> qkv, qkv_sum, wi, wi_sum;
+};
+
 struct DeviceModel {
     int device = -1;
     DeviceBuf params;
     DeviceBuf rope;  // global cos, global sin, local cos, local sin: [rope_len][head_dim / 2] each
     int rope_len = 0;
     DeviceBuf work;
+    FoldedNorms folded;
 };
 
 }  // namespace
@@ -615,6 +628,65 @@ int ensure_device(Model &m, DeviceModel **out) {
     }
     *out = slot.get();
     return RAYA_OK;
+}
+
+// The folding is exact algebra: LN(x) W^T = rstd (x - mean) (g * W)^T with g the norm's gain,
+// i.e. rstd (x (g * W)^T - mean colsum).  Built on the host once per device (the products
+// g_t W[j][t] in f32, the row sums in f64), only when every chunk of a row is whole.
+bool norms_foldable(const Config &c) { return c.hidden % 64 == 0; }
+
+int ensure_folded(const Model &m, DeviceModel &dm) {
+    const Config &c = m.cfg;
+    if (!dm.folded.qkv.empty() || !norms_foldable(c)) return RAYA_OK;
+    const uint64_t d = c.hidden, n3 = 3 * d, n2 = 2 * c.inter;
+    std::vector<float> host;
+    host.reserve((size_t)c.layers * (n3 * d + n3 + n2 * d + n2));
+    FoldedNorms &f = dm.folded;
+    auto fold = [&](const std::string &w, const std::string &gain, uint64_t rows, std::vector<size_t> &off,
+                    std::vector<size_t> &off_sum) {
+        const float *wp = m.w.host.data() + m.w.entries[m.w.index.at(w)].offset;
+        const float *gp = m.w.host.data() + m.w.entries[m.w.index.at(gain)].offset;
+        off.push_back(host.size());
+        for (uint64_t j = 0; j < rows; ++j)
+            for (uint64_t t = 0; t < d; ++t) host.push_back(wp[j * d + t] * gp[t]);
+        off_sum.push_back(host.size());
+        const float *fw = host.data() + off.back();
+        for (uint64_t j = 0; j < rows; ++j) {
+            double sum = 0.0;
+            for (uint64_t t = 0; t < d; ++t) sum += fw[j * d + t];
+            host.push_back((float)sum);
+        }
+    };
+    for (uint64_t i = 0; i < c.layers; ++i) {
+        const std::string p = "encoder.layers." + std::to_string(i);
+        if (i > 0) {
+            fold(p + ".attn.Wqkv.weight", p + ".attn_norm.weight", n3, f.qkv, f.qkv_sum);
+        } else {
+            f.qkv.push_back(0);
+            f.qkv_sum.push_back(0);
+        }
+        fold(p + ".mlp.Wi.weight", p + ".mlp_norm.weight", n2, f.wi, f.wi_sum);
+    }
+    // An empty f.qkv means "not built": on a failure the offsets are cleared, so the next
+    // call builds again.
+    int rc = f.buf.reserve(host.size() * sizeof(float));
+    hipError_t e = rc ? hipSuccess
+                      : hipMemcpy(f.buf.ptr, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (rc || e != hipSuccess) {
+        f.qkv.clear();
+        f.qkv_sum.clear();
+        f.wi.clear();
+        f.wi_sum.clear();
+        return rc ? rc : fail_device(e, "upload folded norm weights");
+    }
+    return RAYA_OK;
+}
+
+// RAYA_LN_FUSION=0 keeps the LayerNorm kernels (for comparison); otherwise the pre-LN norms
+// are folded whenever the hidden size allows.
+bool fuse_norms(const Config &c) {
+    const char *e = std::getenv("RAYA_LN_FUSION");
+    return norms_foldable(c) && !(e && !std::strcmp(e, "0"));
 }
 
 int ensure_rope(const Model &m, DeviceModel &dm, int len) {
@@ -839,6 +911,8 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     if (rc) return rc;
     DeviceModel &dm = *dmp;
     if ((rc = ensure_rope(m, dm, (int)Lmax))) return rc;
+    const bool fused = fuse_norms(c);
+    if (fused && (rc = ensure_folded(m, dm))) return rc;
     hipStream_t stream = (hipStream_t)stream_ptr;
 
     const uint64_t inter = c.inter, big = std::max(inter, c.head_ffn), nact = c.n_act;
@@ -860,6 +934,8 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         probe.take<float>(B * (d + 4));  // act input
         probe.take<float>(B * 256);      // act hidden
         probe.take<float>(B * nact);     // act logits
+        probe.take<float>(T * (d / 64) * 2);  // LayerNorm chunk statistics of h
+        probe.take<float>(T * 2);             // and each row's (mean, rstd)
         need = probe.off;
     }
     if ((rc = dm.work.reserve(need))) return rc;
@@ -875,6 +951,8 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     float *d_feat = cv.take<float>(B * 4), *d_pooled = cv.take<float>(B * d);
     float *act_in = cv.take<float>(B * (d + 4)), *act_hid = cv.take<float>(B * 256);
     float *d_act = cv.take<float>(B * nact);
+    float2 *hstats = (float2 *)cv.take<float>(T * (d / 64) * 2);
+    float2 *hrow = (float2 *)cv.take<float>(T * 2);
     const int32_t *d_ids = d_ints + o_ids, *d_pos = d_ints + o_pos, *d_rowseq = d_ints + o_rs;
     const int32_t *d_start = d_ints + o_start, *d_valid = d_ints + o_valid, *d_qtype = d_ints + o_q;
     const int32_t *d_mrow = d_ints + o_mrow;
@@ -972,6 +1050,30 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         TRY_HIP(launch_gemm(g, stream), "gemm");
         return RAYA_OK;
     };
+    // The residual GEMMs of an encoder layer: h += a W^T, and with fused norms also the
+    // LayerNorm chunk statistics of the new h for the next GEMM.
+    auto gemm_residual = [&](const float *a, uint64_t k, const float *wt, bool stats) -> int {
+        GemmLaunch g{};
+        g.out = h;
+        g.ldo = (int64_t)d;
+        g.a = a;
+        g.lda = (int64_t)k;
+        g.b = wt;
+        g.ldb = (int64_t)k;
+        g.m = (int32_t)T;
+        g.n = (int32_t)d;
+        g.k = (int32_t)k;
+        g.n_rows_b = (int32_t)d;
+        g.act = RAYA_EPI_NONE;
+        g.residual = h;
+        g.ldr = (int64_t)d;
+        g.out_stats = stats ? hstats : nullptr;
+        TRY_HIP(launch_gemm(g, stream), "residual gemm");
+        if (stats)
+            TRY_HIP(launch_ln_stats(hstats, (int)T, (int)(d / 64), (float)c.norm_eps, hrow, stream), "ln stats");
+        return RAYA_OK;
+    };
+    const float *folded = (const float *)dm.folded.buf.ptr;
     auto layer_norm = [&](const float *x, const int32_t *gather, const float *wt, const float *bias, float eps,
                           uint64_t rows, float *o, const float *add, float *o_add) -> int {
         LayerNormLaunch l{};
@@ -1034,7 +1136,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         const std::string sn = name;
         SPAN(1, sn, sp_stage);
         const float *x = h;
-        if (i > 0) {
+        if (i > 0 && !fused) {
             SPAN(2, sn + "/attn_norm", sp_op);
             RECORD(layer_norm(h, nullptr, P(p + ".attn_norm.weight"), nullptr, eps, T, nb, nullptr, nullptr));
             SPAN_END(sp_op);
@@ -1043,27 +1145,36 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         SPAN(2, sn + "/qkv", sp_op);
         const bool global = c.is_global(i);
         const float *cos_t = rope_t + (global ? 0 : 2) * rope_one, *sin_t = cos_t + rope_one;
-        if (hd == (uint64_t)kRopeHeadDim) {
+        {
+            // attn_norm (layers >= 1) folded in when fused: h's statistics from the last
+            // layer's MLP residual GEMM.
+            const bool norm_in = fused && i > 0;
             GemmLaunch g{};
             g.out = qkv;
             g.ldo = (int64_t)(3 * d);
             g.a = x;
             g.lda = (int64_t)d;
-            g.b = P(p + ".attn.Wqkv.weight");
+            g.b = norm_in ? folded + dm.folded.qkv[i] : P(p + ".attn.Wqkv.weight");
             g.ldb = (int64_t)d;
             g.m = (int32_t)T;
             g.n = (int32_t)(3 * d);
             g.k = (int32_t)d;
             g.n_rows_b = g.n;
             g.act = RAYA_EPI_NONE;
-            g.rope_cos = cos_t;
-            g.rope_sin = sin_t;
-            g.positions = d_pos;
-            g.rope_cols = (int32_t)(2 * d);
+            if (norm_in) {
+                g.in_stats = hrow;
+                g.colsum = folded + dm.folded.qkv_sum[i];
+            }
+            if (hd == (uint64_t)kRopeHeadDim) {
+                g.rope_cos = cos_t;
+                g.rope_sin = sin_t;
+                g.positions = d_pos;
+                g.rope_cols = (int32_t)(2 * d);
+            }
             TRY_HIP(launch_gemm(g, stream), "qkv gemm");
-        } else {
-            RECORD(gemm(qkv, 3 * d, x, d, P(p + ".attn.Wqkv.weight"), T, 3 * d, d, RAYA_EPI_NONE, nullptr, nullptr));
-            TRY_HIP(launch_rope(qkv, (int64_t)(3 * d), d_pos, cos_t, sin_t, (int)T, (int)d, (int)hd, stream), "rope");
+            if (hd != (uint64_t)kRopeHeadDim)
+                TRY_HIP(launch_rope(qkv, (int64_t)(3 * d), d_pos, cos_t, sin_t, (int)T, (int)d, (int)hd, stream),
+                        "rope");
         }
         SPAN_END(sp_op);
         SPAN(2, sn + "/attention", sp_op);
@@ -1071,16 +1182,37 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         else RECORD(attend(qkv, c.heads, hd, local_kind, local_arg));
         SPAN_END(sp_op);
         SPAN(2, sn + "/attn_out", sp_op);
-        RECORD(gemm(h, d, ctx, d, P(p + ".attn.Wo.weight"), T, d, d, RAYA_EPI_NONE, nullptr, h));
+        RECORD(gemm_residual(ctx, d, P(p + ".attn.Wo.weight"), fused));
         SPAN_END(sp_op);
-        SPAN(2, sn + "/mlp_norm", sp_op);
-        RECORD(layer_norm(h, nullptr, P(p + ".mlp_norm.weight"), nullptr, eps, T, nb, nullptr, nullptr));
-        SPAN_END(sp_op);
+        if (!fused) {
+            SPAN(2, sn + "/mlp_norm", sp_op);
+            RECORD(layer_norm(h, nullptr, P(p + ".mlp_norm.weight"), nullptr, eps, T, nb, nullptr, nullptr));
+            SPAN_END(sp_op);
+        }
         SPAN(2, sn + "/mlp_in_geglu", sp_op);
-        RECORD(gemm(gated, inter, nb, d, P(p + ".mlp.Wi.weight"), T, inter, d, RAYA_EPI_GEGLU, nullptr, nullptr));
+        if (fused) {  // mlp_norm folded in: h's statistics from the attention residual GEMM
+            GemmLaunch g{};
+            g.out = gated;
+            g.ldo = (int64_t)inter;
+            g.a = h;
+            g.lda = (int64_t)d;
+            g.b = folded + dm.folded.wi[i];
+            g.ldb = (int64_t)d;
+            g.m = (int32_t)T;
+            g.n = (int32_t)inter;
+            g.k = (int32_t)d;
+            g.n_rows_b = (int32_t)(2 * inter);
+            g.act = RAYA_EPI_GEGLU;
+            g.in_stats = hrow;
+            g.colsum = folded + dm.folded.wi_sum[i];
+            TRY_HIP(launch_gemm(g, stream), "mlp in gemm");
+        } else {
+            RECORD(gemm(gated, inter, nb, d, P(p + ".mlp.Wi.weight"), T, inter, d, RAYA_EPI_GEGLU, nullptr, nullptr));
+        }
         SPAN_END(sp_op);
         SPAN(2, sn + "/mlp_out", sp_op);
-        RECORD(gemm(h, d, gated, inter, P(p + ".mlp.Wo.weight"), T, d, inter, RAYA_EPI_NONE, nullptr, h));
+        // the last layer's h goes to the final norm, a kernel of its own
+        RECORD(gemm_residual(gated, inter, P(p + ".mlp.Wo.weight"), fused && i + 1 < c.layers));
         SPAN_END(sp_op);
         SPAN_END(sp_stage);
         RECORD(record_rows(sn.c_str(), h, d));

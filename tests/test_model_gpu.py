@@ -136,9 +136,11 @@ def random_batch(rng, cfg, b, seq, k):
     return ids, valid, pos, mask, qtype
 
 
-@pytest.mark.parametrize("hidden,heads", [(128, 2), (64, 2), (256, 4)])
+@pytest.mark.parametrize("hidden,heads", [(128, 2), (64, 2), (256, 4), (96, 2)])
 def test_batch_matches_oracle_per_sequence(tmp_path, hidden, heads):
-    """hidden 256: the row-in-registers LayerNorm (rows of a multiple of 256 floats)."""
+    """hidden 256: the row-in-registers LayerNorm (rows of a multiple of 256 floats); hidden 96:
+    not a multiple of 64, so the LayerNorms stay kernels of their own (the others fold them
+    into the GEMMs)."""
     cfg, cdir, w = make_model(tmp_path, hidden, heads)
     model = M.Model.load(cdir)
     rng = np.random.default_rng(hidden)
@@ -205,11 +207,12 @@ def test_stage_timing_spans_and_outputs_unchanged():
     model.set_profiling(2)
     out2 = model.forward(inp)
     names2 = [n for n, _ in model.stage_times()]
-    ops = ["qkv", "attention", "attn_out", "mlp_norm", "mlp_in_geglu", "mlp_out"]
+    # the fixture's width (a multiple of 64) folds both LayerNorms into the GEMMs that read them
+    ops = ["qkv", "attention", "attn_out", "mlp_in_geglu", "mlp_out"]
     for i in range(cfg.layers):
         layer = f"encoder_layer_{i:02d}"
         subs = [n.split("/")[1] for n in names2 if n.startswith(layer + "/")]
-        assert subs == (["attn_norm"] if i > 0 else []) + ops, (layer, subs)
+        assert subs == ops, (layer, subs)
     times = dict(model.stage_times())
     for i in range(cfg.layers):
         layer = f"encoder_layer_{i:02d}"
@@ -256,3 +259,28 @@ def test_base_width_layers_match_oracle(tmp_path):
             assert err.max() <= 1e-4 and rel <= 1e-5, (i, name, float(err.max()), rel)
         dz = float(np.abs(out.logits[i] - want.logits).max())
         assert np.abs(out.probabilities[i] - want.probabilities).max() <= dz / 2 + 1e-6, dz
+
+
+@pytest.mark.parametrize("case", ["medium", "padded"])
+def test_folded_norms_match_the_layernorm_kernels(case, monkeypatch):
+    """The pre-LN LayerNorms folded into the GEMMs (statistics from the residual GEMM,
+    normalisation in the next GEMM's epilogue) against the LayerNorm kernels
+    (RAYA_LN_FUSION=0) on the same model: every stage within the goldens' 1e-5, both paths
+    within 1e-5 of the golden."""
+    cfg, model, g, valid = load_case(case)
+    inp = golden_input(g, valid)
+    fused = M.Trace()
+    model.forward(inp, trace=fused)
+    monkeypatch.setenv("RAYA_LN_FUSION", "0")
+    plain = M.Trace()
+    model.forward(inp, trace=plain)
+    seq = g["input_ids"].shape[1]
+    worst = 0.0
+    for name, tol in stages(cfg):
+        a, b = fused.get(name)[1], plain.get(name)[1]
+        if a.ndim == 3 and a.shape[1] == seq:
+            a, b = a[:, :valid], b[:, :valid]
+        err = float(np.abs(a - b).max())
+        worst = max(worst, err)
+        assert err <= tol, (name, err)
+    print(f"{case}: folded vs kernel LayerNorm, worst stage difference {worst:.2e}", flush=True)
