@@ -32,7 +32,11 @@ With the default workload the line also carries:
 * "encoder_layer": one block-local layer of that model on B=16 x L=1024 valid
   tokens (BlockDiag(64) on the local layers), from the forward's own per-layer
   event spans;
-* "encoder_gemms": the encoder's four GEMM shapes alone.
+* "encoder_gemms": the encoder's four GEMM shapes alone;
+* "postln_layer": one post-LN encoder layer as BERT writes it (hidden 768 = 12 x 64,
+  biases, erf-GELU feed-forward 3072, LayerNorm eps 1e-12 after each residual add)
+  on B=16 x L=1024 tokens with BlockDiag(64) attention, N(0, 0.02) weights, zero
+  biases, unit gains and N(0, 1) inputs, and the oracle's CPU layer on one sequence.
 
 --refbench writes the reference bench's result document
 (crates/raya-kernels/benches/local_attention.rs:89-172): label, metadata and one
@@ -54,8 +58,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 from raya_amd.workloads import (ATTENTION as WORKLOADS, DEFAULT_ATTENTION as DEFAULT, ENCODER,  # noqa: E402
-                                ENCODER_WEIGHT_SEED, LAYER, REF_BLOCK, algorithmic, attention_inputs,
-                                encoder_inputs, mask_name)
+                                ENCODER_WEIGHT_SEED, LAYER, POSTLN_LAYER, REF_BLOCK, algorithmic,
+                                attention_inputs, encoder_inputs, mask_name, postln_flops, postln_inputs)
 
 PEAK_HBM_GBS = 8000.0
 PEAK_FP32_MFMA_TFLOPS = 157.3
@@ -530,6 +534,67 @@ def encoder_cpu_baseline(ckpt, ids, valid, pos, mask, qtype, gpu_out, budget_s: 
 
 
 
+def bench_postln(steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dict:
+    """One post-LN layer (raya_postln_layer_forward: QKV GEMM + bias, attention reading the
+    packed qkv, Wo GEMM + bias + residual, LayerNorm, W1 GEMM + bias + GELU, W2 GEMM + bias +
+    residual, LayerNorm) on the whole batch with its inputs resident in HBM: K back-to-back
+    forwards bracketed by one event pair on the launch stream."""
+    import numpy as np
+    import torch
+
+    from raya_amd import Mask
+    from raya_amd.layers import PostLNLayer
+
+    spec = POSTLN_LAYER
+    x, valid, w = postln_inputs(spec)
+    layer = PostLNLayer({k: torch.from_numpy(v).cuda() for k, v in w.items()}, spec["heads"], spec["eps"],
+                        Mask.block_diag(spec["block"]))
+    xd, vd = torch.from_numpy(x).cuda(), torch.from_numpy(valid).cuda()
+    out = torch.empty_like(xd)
+    stream = torch.cuda.current_stream()
+    log(f"post-LN layer: warmup {warmup}, timing {steps} forwards (B={spec['batch']}, L={spec['seq']})")
+    for _ in range(warmup):
+        layer.forward(xd, vd, out, stream=stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        layer.forward(xd, vd, out, stream=stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gemm, attn = postln_flops(spec, valid)
+    res = {
+        "workload": spec["workload"], "batch": spec["batch"], "seq": spec["seq"], "hidden": spec["hidden"],
+        "heads": spec["heads"], "ffn": spec["ffn"], "ln_eps": spec["eps"], "mask": f"block_diag({spec['block']})",
+        "ms_per_layer": ms, "sequences_per_s": spec["batch"] / (ms / 1e3), "flop_per_layer": gemm + attn,
+        "tflops": (gemm + attn) / (ms / 1e3) / 1e12,
+        "mfma_frac": (gemm + attn) / (ms / 1e3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+        "timing": f"{steps} back-to-back forwards between two events on the launch stream",
+        "weights": "N(0, 0.02), zero biases, LayerNorm gain 1 and shift 0; x N(0, 1)",
+    }
+    if cpu:
+        from oracle import forward as F
+
+        import oracle
+
+        got = out.cpu().numpy()
+        F.GEMM_THREADS = cpu_threads()
+        done, diff, t0 = 0, 0.0, time.perf_counter()
+        while done < spec["batch"]:
+            want = F.postln_layer(x[done], int(valid[done]), w, spec["heads"], spec["eps"], oracle.MASK_BLOCKDIAG,
+                                  spec["block"])
+            diff = max(diff, float(np.abs(got[done] - want).max()))
+            done += 1
+            if time.perf_counter() - t0 > cpu_seconds:
+                break
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": done / dt, "unit": "sequences/s", "cores": F.GEMM_THREADS, "kind": "port",
+                               "sample": f"first {done} sequences of the batch, one at a time, {dt:.1f} s",
+                               "gpu_vs_cpu_max_abs": diff}
+    return res
+
+
 # --- the reference bench's document -------------------------------------------------------------
 
 def refbench(out_path: str | None, samples: int, naive_samples: int, cpu: bool) -> dict:
@@ -718,6 +783,8 @@ def main() -> int:
             result["encoder_layer"] = layer
         log("encoder gemm shapes")
         result["encoder_gemms"] = bench_gemms(20, 3)
+        result["postln_layer"] = bench_postln(args.encoder_steps, args.encoder_warmup, min(args.cpu_seconds, 3.0),
+                                              cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -205,6 +205,37 @@ int raya_matmul_nt_device(float *out, int64_t ldo, const float *a, int64_t lda, 
                           int64_t ldb, uint64_t m, uint64_t n, uint64_t k,
                           const raya_gemm_epilogue *ep, void *stream);
 
+/* ---- A post-LN encoder layer ----------------------------------------------------------------
+ *
+ * No counterpart in the reference, whose encoder layer is pre-LN (encoder::layer,
+ * crates/raya-core/src/encoder.rs:96-152): BERT's layer, i.e. nn.TransformerEncoderLayer with
+ * norm_first=False, GELU (erf) and biases, as a block-local encoder layer is usually written:
+ *   y1  = LayerNorm1(x + Attn(x Wqkv^T + bqkv) Wo^T + bo)
+ *   out = LayerNorm2(y1 + gelu(y1 W1^T + b1) W2^T + b2)
+ * Attention uses the mask (mask_kind, mask_arg) and the per-sequence valid lengths, scale
+ * 1/sqrt(head_dim); its rows at or beyond valid_len are zero, as Naive::attend's.  Weights are
+ * device pointers in nn.Linear's [out_features][in_features] layout (wqkv: q, k and v stacked,
+ * [3 hidden][hidden]); any bias may be NULL (zero).  LayerNorm eps is ln_eps. */
+typedef struct raya_postln_layer {
+    uint64_t batch, seq, hidden, heads, ffn;
+    int32_t mask_kind;
+    int32_t reserved; /* must be 0 */
+    uint64_t mask_arg;
+    float ln_eps;
+    const float *wqkv, *bqkv, *wo, *bo, *ln1_w, *ln1_b, *w1, *b1, *w2, *b2, *ln2_w, *ln2_b;
+} raya_postln_layer;
+
+/* Device workspace the layer needs (qkv, context, sums, y1, feed-forward activations: batch *
+ * seq * (6 hidden + ffn) floats), or 0 when the layer description is invalid. */
+uint64_t raya_postln_workspace_bytes(const raya_postln_layer *layer);
+
+/* x and out: device [batch][seq][hidden] fp32 (16-byte aligned), valid_len: device int32
+ * [batch]; workspace: device, at least raya_postln_workspace_bytes.  Asynchronous on `stream`.
+ * Every row of out is computed; rows at or beyond a sequence's valid length attend to nothing
+ * (their attention output is zero). */
+int raya_postln_layer_forward(const raya_postln_layer *layer, const int32_t *valid_len, const float *x, float *out,
+                              void *workspace, uint64_t workspace_bytes, void *stream);
+
 /* ---- Decision model (crates/raya-core, crates/raya-weights) ------------------------------
  *
  * Errors of this part are raya_core::Error (crates/raya-core/src/error.rs:5-33); the

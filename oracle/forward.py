@@ -118,6 +118,24 @@ def attend(qkv, heads, hd, theta, kind, arg, valid_len):
     return np.ascontiguousarray(out.transpose(1, 0, 2).reshape(seq, heads * hd))
 
 
+def postln_layer(x, valid_len: int, w: dict, heads: int, eps: float, kind: int, arg: int):
+    """One post-LN encoder layer on one sequence (x: [seq, hidden] float32), the layer of
+    raya_postln_layer_forward, restated with the reference's building blocks: sequential-f32
+    linear with bias (ops.rs:91-109), Naive attention without RoPE (naive.rs:13-65), LayerNorm
+    with f64 statistics (ops.rs:51-74) and erf GELU (ops.rs:7-38).  `w` holds wqkv [3d, d]
+    (q, k, v stacked), wo [d, d], w1 [F, d], w2 [d, F], ln1_w/ln2_w [d] and optional biases
+    bqkv, bo, b1, b2, ln1_b, ln2_b.  Rows at or beyond valid_len attend to nothing."""
+    x = np.asarray(x, np.float32)
+    d = x.shape[1]
+    hd = d // heads
+    eps = np.float32(eps)
+    qkv = linear(x, w["wqkv"], w.get("bqkv"))
+    ctx = attend(qkv, heads, hd, None, kind, arg, valid_len)
+    y1 = oracle.layer_norm(x + linear(ctx, w["wo"], w.get("bo")), w["ln1_w"], w.get("ln1_b"), eps)
+    f = oracle.gelu_array(linear(y1, w["w1"], w.get("b1")))
+    return oracle.layer_norm(y1 + linear(f, w["w2"], w.get("b2")), w["ln2_w"], w.get("ln2_b"), eps)
+
+
 def f32_sum(xs) -> np.float32:
     acc = np.float32(0.0)
     for x in xs:

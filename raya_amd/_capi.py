@@ -66,6 +66,14 @@ class ModelInfoC(ctypes.Structure):
                                         "param_floats")]
 
 
+class PostLNLayerC(ctypes.Structure):
+    _fields_ = [("batch", ctypes.c_uint64), ("seq", ctypes.c_uint64), ("hidden", ctypes.c_uint64),
+                ("heads", ctypes.c_uint64), ("ffn", ctypes.c_uint64), ("mask_kind", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("mask_arg", ctypes.c_uint64), ("ln_eps", ctypes.c_float)]
+    _fields_ += [(n, ctypes.c_void_p) for n in ("wqkv", "bqkv", "wo", "bo", "ln1_w", "ln1_b", "w1", "b1",
+                                                 "w2", "b2", "ln2_w", "ln2_b")]
+
+
 class ForwardBatchC(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_uint64), ("seq", ctypes.c_uint64), ("markers", ctypes.c_uint64),
                 ("input_ids", ctypes.c_void_p), ("valid_len", ctypes.c_void_p),
@@ -115,6 +123,8 @@ SIGNATURES = [
     ("raya_matmul_nt", ctypes.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _u64, _u64, _u64]),
     ("raya_matmul_nt_device", ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _u64, _u64, _u64,
                                              ctypes.POINTER(GemmEpilogueC), _vp]),
+    ("raya_postln_workspace_bytes", ctypes.c_uint64, [ctypes.POINTER(PostLNLayerC)]),
+    ("raya_postln_layer_forward", ctypes.c_int, [ctypes.POINTER(PostLNLayerC), _vp, _vp, _vp, _vp, _u64, _vp]),
     ("raya_model_load", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     ("raya_model_free", None, [_vp]),
     ("raya_expected_params", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ParamEntryC), _u64,

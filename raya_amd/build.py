@@ -19,7 +19,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libraya_hip.so")
-SOURCES = ["attention.hip", "gemm.hip", "encoder.hip", "capi.cpp", "model.cpp"]
+SOURCES = ["attention.hip", "gemm.hip", "encoder.hip", "capi.cpp", "model.cpp", "postln.cpp"]
 ARCH = "gfx950"
 
 

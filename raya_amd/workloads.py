@@ -121,3 +121,40 @@ def encoder_inputs(spec):
     mask = np.ones((b, k), np.uint8)
     qtype = np.full(b, spec["qtype"], np.uint64)
     return ids, valid, pos, mask, qtype
+
+
+POSTLN_LAYER = {
+    # one post-LN encoder layer as BERT writes it: hidden 768 = 12 x 64, GELU feed-forward 3072,
+    # LayerNorm eps 1e-12, weights N(0, 0.02), zero biases, LayerNorm gain 1 and shift 0,
+    # inputs N(0, 1), 16 sequences of 1024 valid tokens, BlockDiag(64) attention
+    "workload": "postln_layer_b16_l1024_768_gelu3072_blockdiag64",
+    "family": 3, "batch": 16, "seq": 1024, "hidden": 768, "heads": 12, "ffn": 3072, "eps": 1e-12,
+    "block": 64, "std": 0.02,
+}
+
+
+def postln_flops(spec, valid) -> tuple[int, int]:
+    """(GEMM FLOP, attention FLOP) of one post-LN layer over the valid tokens: 2 d (3d + d + 2F)
+    per token, and 4 D H per allowed (query, key) pair under BlockDiag(block)."""
+    d, f, h = spec["hidden"], spec["ffn"], spec["heads"]
+    tokens = int(sum(int(v) for v in valid))
+    gemm = tokens * 2 * d * (3 * d + d + 2 * f)
+    attn = 4 * (d // h) * h * sum(key_pairs(("block_diag", spec["block"]), int(v)) for v in valid)
+    return gemm, attn
+
+
+def postln_inputs(spec):
+    """(x [B, L, d] float32, valid [B] int32, weights) of a post-LN layer workload: x N(0, 1)
+    (stream 0 of the family), the four weight matrices N(0, std) (streams 5, 7, 8, 9), zero
+    biases, LayerNorm gains 1 and shifts 0."""
+    c, b, s, d, f = spec["family"], spec["batch"], spec["seq"], spec["hidden"], spec["ffn"]
+    x = synth.normal(synth.workload_seed(c, 0), b * s * d).reshape(b, s, d)
+    valid = np.full(b, s, np.int32)
+    std = np.float32(spec["std"])
+    w = {}
+    for name, shape, stream in (("wqkv", (3 * d, d), 5), ("wo", (d, d), 7), ("w1", (f, d), 8), ("w2", (d, f), 9)):
+        w[name] = (synth.normal(synth.workload_seed(c, stream), shape[0] * shape[1]) * std).reshape(shape)
+    w.update({"bqkv": np.zeros(3 * d, np.float32), "bo": np.zeros(d, np.float32), "b1": np.zeros(f, np.float32),
+              "b2": np.zeros(d, np.float32), "ln1_w": np.ones(d, np.float32), "ln1_b": np.zeros(d, np.float32),
+              "ln2_w": np.ones(d, np.float32), "ln2_b": np.zeros(d, np.float32)})
+    return x, valid, w

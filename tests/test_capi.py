@@ -222,3 +222,22 @@ def test_gemm_device_arguments_are_checked_before_any_launch():
         g.matmul_nt_device(out, a, b, residual=torch.zeros(n, m).t())
     with pytest.raises(TypeError, match="GPU"):  # host tensors never reach the library
         g.matmul_nt_device(out, a, b, bias=torch.zeros(n), residual=torch.zeros(m, n))
+
+
+def test_postln_layer_checks_before_any_gpu_work():
+    """The post-LN layer rejects bad shapes and a short workspace without touching the GPU."""
+    lib = C.lib()
+    desc = C.PostLNLayerC(2, 16, 64, 2, 128, C.RAYA_MASK_BLOCKDIAG, 0, 16, 1e-5)
+    for name in ("wqkv", "wo", "w1", "w2", "ln1_w", "ln2_w"):
+        setattr(desc, name, 256)  # never dereferenced: the checks fail first
+    need = lib.raya_postln_workspace_bytes(ctypes.byref(desc))
+    assert need == 2 * 16 * (6 * 64 + 128) * 4
+    rc = lib.raya_postln_layer_forward(ctypes.byref(desc), 256, 256, 256, 256, need - 4, None)
+    assert rc == C.RAYA_ERR_SHAPE and "workspace" in C.last_error().message.decode()
+    bad = C.PostLNLayerC(2, 16, 60, 4, 128, C.RAYA_MASK_BLOCKDIAG, 0, 16, 1e-5)  # head_dim 15
+    assert lib.raya_postln_workspace_bytes(ctypes.byref(bad)) == 0
+    assert lib.raya_postln_layer_forward(ctypes.byref(bad), 256, 256, 256, 256, 1 << 30, None) == C.RAYA_ERR_SHAPE
+    odd = C.PostLNLayerC(2, 16, 64, 2, 128, 9, 0, 16, 1e-5)
+    for name in ("wqkv", "wo", "w1", "w2", "ln1_w", "ln2_w"):
+        setattr(odd, name, 256)
+    assert lib.raya_postln_layer_forward(ctypes.byref(odd), 256, 256, 256, 256, 1 << 30, None) == C.RAYA_ERR_UNSUPPORTED
