@@ -76,6 +76,10 @@ struct Plan {
 
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroup i runs on XCD i mod 8
 
+// Row strides (floats) below which the balanced Window64 steps form their
+// K/V offsets (up to 191 rows plus a row's last chunk) in 31 bits.
+constexpr int64_t kMaxBalancedRowStride = (int64_t(1) << 31) / (4 * 3 * 64) - 64;
+
 // Mask::key_range (attention.rs:48-59) plus BlockDiag, clipped to valid.
 // mask_arg was clamped to seq by the host, so no sum below overflows int32
 // for seq < 2^30.
@@ -330,19 +334,21 @@ __device__ __forceinline__ void qk_tile(const float *ks, const float (&qreg)[DP 
     }
 }
 
-// Masks scores outside [lo, hi) (tile-relative, already offset by g) when
-// need_mask, folds the tile into the running max m and partial sum l
-// (rescaling oacc unless first), and turns the scores into weights.
+// Masks scores outside [lo0, hi0) in the even subtiles and [lo1, hi1) in
+// the odd ones (tile-relative, already offset by g) when need_mask, folds the
+// tile into the running max m and partial sum l (rescaling oacc unless
+// first), and turns the scores into weights.
 template <int NT>
 __device__ __forceinline__ void softmax_tile(floatx4 (&sacc)[4], floatx4 (&oacc)[NT], float &m, float &l,
-                                             bool first, bool need_mask, int lo, int hi, float c_exp) {
+                                             bool first, bool need_mask, int lo0, int hi0, int lo1, int hi1,
+                                             float c_exp) {
     if (need_mask) {
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int j = 16 * t + 4 * r;
-                if (j < lo || j >= hi) sacc[t][r] = -INFINITY;
+                if (j < (t & 1 ? lo1 : lo0) || j >= (t & 1 ? hi1 : hi0)) sacc[t][r] = -INFINITY;
             }
     }
     float tmax = sacc[0][0];
@@ -611,19 +617,21 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // out-of-range parts are zeroed after the wait), then V, which is only
     // waited for after QK^T and the softmax.
     float qreg[DQ];
-    // Operands of one tile's asm issue: this wave's K and V source rows and LDS slots.
     // Operands of one tile's asm issue: scalar bases at the tile's first row, 32-bit
-    // byte offsets of this wave's chunks (rows past the tile's keys clamped to its
-    // last row) and the LDS slots.
-    const auto tile_addrs = [&](int kt, const float *&kbase, uint32_t ko[4], uint32_t kl[4],
+    // byte offsets of this wave's chunks (rows past the item's keys clamped to its
+    // last row) and the LDS slots.  The tile's even 16-key subtiles are keys
+    // kx + 16t .., its odd ones ky + 16t .. (kx = ky but in the balanced steps
+    // below).
+    const auto tile_addrs = [&](int kx, int ky, const float *&kbase, uint32_t ko[4], uint32_t kl[4],
                                 const float *&vbase, uint32_t vo[4], uint32_t vl[4]) {
-        const int last = min(kt + kKeys, it.k_hi) - 1 - kt;
-        kbase = kb + (int64_t)kt * a.k_rs;
-        vbase = vb + (int64_t)kt * a.v_rs;
+        const int k0 = min(kx, ky);
+        kbase = kb + (int64_t)k0 * a.k_rs;
+        vbase = vb + (int64_t)k0 * a.v_rs;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int slot = (wave * LPW + j) * 64 + lane;
-            const int r = min(slot / CH, last), c = swz<CH>(slot % CH, slot / CH);
+            const int lrow = slot / CH, c = swz<CH>(slot % CH, lrow);
+            const int r = min(((lrow >> 4) & 1 ? ky : kx) + lrow, it.k_hi - 1) - k0;
             ko[j] = (uint32_t)(r * (int)a.k_rs * 4 + 16 * c);
             vo[j] = (uint32_t)(r * (int)a.v_rs * 4 + 16 * c);
             const int lds_off = (wave * LPW + j) * 64 * 16;
@@ -631,11 +639,48 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             vl[j] = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)((char *)vs + lds_off));
         }
     };
+    // The item's n tiles are walked starting from the one whose global index
+    // (k / 64) is a multiple of n, then on around.  The items running together
+    // then touch, in each step, only the tiles of one residue mod n: an item's
+    // neighbours share its tiles (Window64: 3, Block3: 6), so the first touches
+    // of a tile, which go to HBM, spread over all n steps instead of all landing
+    // in the first, and overlap the other steps' arithmetic.  The softmax is
+    // independent of the order.
+    const int n_tiles = (it.k_hi - it.k_lo + kKeys - 1) / kKeys;
+    int rot = 0;
+    if (n_tiles > 1) {
+        rot = (it.k_lo / kKeys) % n_tiles;
+        rot = rot == 0 ? 0 : n_tiles - rot;
+    }
+    const auto tile_at = [&](int j) {
+        j += rot;
+        return it.k_lo + (j >= n_tiles ? j - n_tiles : j) * kKeys;
+    };
+    // Window64 and Sliding(64) items away from the sequence ends span exactly
+    // three whole tiles, and wave w's rows meet 4 - w, 4 and w + 1 of their
+    // subtiles: walked tile by tile, each step waits for its busiest wave (12
+    // subtile steps per item for 9 subtiles of work per wave).  Balanced steps
+    // pair the two edge tiles' halves instead: tile 0's even subtiles with tile
+    // 2's odd ones, tile 1, then the other halves; every wave then meets 2, 4
+    // and 3 subtiles.  Any mask stays exact: subtiles are scored at their own
+    // keys.  The offsets of the paired step reach 191 rows of the row stride.
+    const bool balanced = FUSED && SKIP && n_tiles == 3 && it.k_hi - it.k_lo == 3 * kKeys &&
+                          a.k_rs < kMaxBalancedRowStride && a.v_rs < kMaxBalancedRowStride;
+    const auto step_keys = [&](int kt, int &kx, int &ky) {
+        kx = ky = kt;
+        if (balanced && kt != it.k_lo + kKeys) {
+            kx = kt == it.k_lo ? it.k_lo : it.k_lo + 2 * kKeys;
+            ky = kt == it.k_lo ? it.k_lo + 2 * kKeys : it.k_lo;
+        }
+    };
+    const int kt0 = tile_at(0);
     if constexpr (FUSED) {
         // K, Q and V in one asm block that ends waiting for K and Q only.
         const float *kbase, *vbase;
         uint32_t ko[4], kl[4], vo[4], vl[4];
-        tile_addrs(it.k_lo, kbase, ko, kl, vbase, vo, vl);
+        int kx, ky;
+        step_keys(kt0, kx, ky);
+        tile_addrs(kx, ky, kbase, ko, kl, vbase, vo, vl);
         const float *qa = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)min(qi, valid - 1) * a.q_rs + g * DQ;
         floatx4 q4[4];
         issue_kqv64(kbase, ko, kl, qa, q4, vbase, vo, vl);
@@ -644,7 +689,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
 #pragma unroll
             for (int e = 0; e < 4; ++e) qreg[4 * c + e] = q4[c][e];
     } else {
-        stage(kb, a.k_rs, ks, it.k_lo);
+        stage(kb, a.k_rs, ks, kt0);
         const int qrow = min(qi, valid - 1);
         const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qrow * a.q_rs;
 #pragma unroll
@@ -655,7 +700,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             qreg[4 * c + 2] = x.z;
             qreg[4 * c + 3] = x.w;
         }
-        stage(vb, a.v_rs, vs, it.k_lo);
+        stage(vb, a.v_rs, vs, kt0);
     }
 
     floatx4 oacc[NT];
@@ -669,14 +714,17 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     const int k_row0 = 4 * (li & 3) + (li >> 2);
 
     if constexpr (TIMED) clk->last = clock_now();
-    for (int kt = it.k_lo; kt < it.k_hi; kt += kKeys) {
-        if (kt != it.k_lo) {
+    for (int j = 0; j < n_tiles; ++j) {
+        const int kt = tile_at(j);
+        int kx, ky;
+        step_keys(kt, kx, ky);
+        if (j != 0) {
             // Every wave's LDS reads of the previous tile have returned.
             barrier_after_reads();
             if constexpr (FUSED) {
                 const float *kbase, *vbase;
                 uint32_t ko[4], kl[4], vo[4], vl[4];
-                tile_addrs(kt, kbase, ko, kl, vbase, vo, vl);
+                tile_addrs(kx, ky, kbase, ko, kl, vbase, vo, vl);
                 issue_kv64(kbase, ko, kl, vbase, vo, vl);
             } else {
                 stage(kb, a.k_rs, ks, kt);
@@ -686,7 +734,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         // This wave's K (and Q) loads have landed (the fused issue waited already) ...
         if constexpr (!FUSED) __builtin_amdgcn_s_waitcnt(kWaitAllButV);
         barrier_only();  // ... and every other wave's
-        if (kt == it.k_lo) {
+        if (j == 0) {
             // Q is zero on rows at or beyond valid and on dims at or beyond D; a
             // negative scale is carried by negating Q.
 #pragma unroll
@@ -696,8 +744,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 for (int e = 0; e < 4; ++e) qreg[4 * c + e] = in ? qreg[4 * c + e] * q_sign : 0.f;
             }
         }
-        const bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
-        bool active = rows_active;
+        bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
         // Sliding windows: the 16-key subtiles outside the union of the wave's
         // key intervals [w_first.lo, w_last.hi) hold no live key for any of its
         // rows (about a quarter of an item's subtiles at Window64); such a tile
@@ -707,12 +754,16 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         if constexpr (SKIP || SPLIT) {
             live = 0;
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-                if (kt + 16 * t < w_last.hi && kt + 16 * t + 16 > w_first.lo) live |= 1 << t;
-            if constexpr (SPLIT) live &= 1 << wave;
+            for (int t = 0; t < 4; ++t) {
+                const int k16 = (t & 1 ? ky : kx) + 16 * t;
+                if (k16 < w_last.hi && k16 + 16 > w_first.lo) live |= 1 << t;
+            }
             live = __builtin_amdgcn_readfirstlane(live);
-            if constexpr (SPLIT) active = active && live != 0;
+            // A tile meets the rows' keys exactly when one of its subtiles does.
+            if constexpr (SKIP) rows_active = wave_live && live != 0;
+            if constexpr (SPLIT) live &= 1 << wave;
         }
+        const bool active = SPLIT ? rows_active && live != 0 : rows_active;
         // The keys this wave may score in this tile: the row's interval, and
         // under SPLIT only its own subtile.
         int m_lo = rr.lo, m_hi = rr.hi;
@@ -745,9 +796,9 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             if constexpr (SPLIT) {
                 softmax_sub<NT>(ssub, oacc, m, l, wave, m_lo - kt - g, m_hi - kt - g, c_exp);
             } else {
-                softmax_tile<NT>(sacc, oacc, m, l, kt == it.k_lo,
-                                 !(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi), m_lo - kt - g,
-                                 m_hi - kt - g, c_exp);
+                softmax_tile<NT>(sacc, oacc, m, l, j == 0,
+                                 kx != ky || !(wave_full_rows && kt >= w_last.lo && kt + kKeys <= w_first.hi),
+                                 m_lo - kx - g, m_hi - kx - g, m_lo - ky - g, m_hi - ky - g, c_exp);
             }
             if constexpr (TIMED) {
                 settle(l);

@@ -416,3 +416,53 @@ def test_scale_zero_weighs_allowed_keys_uniformly(hip_attention):
         i = 100
         r = mask.key_range(i, 250)
         assert np.abs(out[:, i] - v[:, r.start:r.stop].mean(axis=1)).max() < 1e-5
+
+
+@pytest.mark.parametrize("name", ["window64", "sliding64"])
+def test_window64_balanced_steps(hip_attention, name):
+    """Window64 / Sliding(64) items away from the sequence ends run three balanced steps
+    (halves of the two edge key tiles paired, then the middle tile); the items at the
+    sequence ends and at each valid length run tile by tile.  Dense and packed layouts
+    against the naive oracle."""
+    b, h, s, d = 3, 2, 1000, 64
+    valid = np.array([1000, 777, 321], np.int32)
+    q, k, v = (synth.normal(31 + i, b * h * s * d).reshape(b, h, s, d) for i in range(3))
+    mask, okind, block, window = MASKS[name]
+    want = oracle.naive_attend_batched(q, k, v, okind, valid, R.kernels.default_scale(d),
+                                       block=block, window=window)
+    out = torch.full((b, h, s, d), 5.0, device="cuda")
+    hip_attention.attend_batched(_dev(q), _dev(k), _dev(v), out, _dev(valid), mask)
+    torch.cuda.synchronize()
+    check_close(out.cpu().numpy(), want, f"dense {name}")
+    packed = np.stack([q, k, v], axis=2).transpose(0, 3, 2, 1, 4).copy()  # b, s, 3, h, d
+    pk = _dev(packed)
+    ctx = torch.full((b, s, h, d), 5.0, device="cuda")
+    lay = {"shape": (b, h, s, d), "q": (s * 3 * h * d, d, 3 * h * d), "k": (s * 3 * h * d, d, 3 * h * d),
+           "v": (s * 3 * h * d, d, 3 * h * d), "out": (s * h * d, d, h * d)}
+    hip_attention.attend_batched(pk[:, :, 0], pk[:, :, 1], pk[:, :, 2], ctx, _dev(valid), mask, layouts=lay)
+    torch.cuda.synchronize()
+    check_close(ctx.cpu().numpy().transpose(0, 2, 1, 3), want, f"packed {name}")
+
+
+def test_window64_row_stride_past_the_balanced_offset_range(hip_attention):
+    """A row stride of 3M floats: inside the fused issue's offset range (8.4M) but past the
+    balanced steps' (2.8M, 191 rows), so the three-tile items walk tile by tile."""
+    s, d, rs = 200, 64, 3_000_000
+    valid = np.array([s], np.int32)
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.standard_normal((1, 1, s, d)).astype(np.float32) for _ in range(3))
+    bufs = []
+    for x in (q, k, v):
+        t = torch.zeros(s * rs, device="cuda")
+        t.view(s, rs)[:, :d] = _dev(x[0, 0])
+        bufs.append(t)
+    out = torch.full((s * rs,), float("nan"), device="cuda")
+    lay = {"shape": (1, 1, s, d), "q": (0, 0, rs), "k": (0, 0, rs), "v": (0, 0, rs), "out": (0, 0, rs)}
+    hip_attention.attend_batched(*bufs, out, _dev(valid), R.Mask.WINDOW64, layouts=lay)
+    torch.cuda.synchronize()
+    got = out.view(s, rs)[:, :d].cpu().numpy()
+    want = oracle.naive_attend_batched(q, k, v, oracle.MASK_WINDOW64, valid, R.kernels.default_scale(d),
+                                       block=128, window=64)
+    check_close(got, want[0, 0], "window64 rs 3M")
+    del bufs, out
+    torch.cuda.empty_cache()
