@@ -411,9 +411,8 @@ GEMM_M = 21405
 
 def bench_gemms(steps: int, warmup: int) -> dict:
     """The encoder's four GEMM shapes alone, with their fused epilogues, inputs resident in
-    HBM: K back-to-back launches per shape bracketed by one event pair on the launch stream.
-    Every shape's warm-up launches run before any shape is timed, so the first one timed
-    does not pay for the clock's ramp from idle."""
+    HBM: K back-to-back launches per shape bracketed by one event pair on the launch stream,
+    after RAMP_MS of back-to-back launches and every shape's warm-up launches."""
     import torch
 
     import raya_amd as R
@@ -423,21 +422,24 @@ def bench_gemms(steps: int, warmup: int) -> dict:
     stream = torch.cuda.current_stream()
     gen = torch.Generator(device="cuda").manual_seed(1000 * 4 + 7)
     res = {"m": GEMM_M, "steps": steps, "warmup": warmup, "shapes": {}}
-    steps_of = {}
+    steps_of, operands = {}, {}
     for name, n, k, epi in GEMM_SHAPES:
         rows = 2 * n if epi == "geglu" else n
         a = torch.randn(GEMM_M, k, device="cuda", generator=gen)
         b = 0.02 * torch.randn(rows, k, device="cuda", generator=gen)
+        operands[name] = (a, b)
         out = torch.randn(GEMM_M, n, device="cuda", generator=gen)
         act = C.RAYA_EPI_GEGLU if epi == "geglu" else C.RAYA_EPI_NONE
         resid = out if epi == "residual" else None
         steps_of[name] = (lambda a=a, b=b, out=out, act=act, resid=resid:
                           g.matmul_nt_device(out, a, b, activation=act, residual=resid, stream=stream))
+    # From idle (as with --gemm-only) the clock needs tens of milliseconds of work to rise.
+    ramp(steps_of[GEMM_SHAPES[0][0]])
     for _ in range(warmup):
         for step in steps_of.values():
             step()
-    for name, n, k, epi in GEMM_SHAPES:
-        step = steps_of[name]
+
+    def timed(step) -> float:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record(stream)
@@ -445,11 +447,39 @@ def bench_gemms(steps: int, warmup: int) -> dict:
             step()
         e1.record(stream)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
+        return e0.elapsed_time(e1) / steps
+
+    for name, n, k, epi in GEMM_SHAPES:
+        ms = timed(steps_of[name])
         flops = 2.0 * GEMM_M * (2 * n if epi == "geglu" else n) * k
         res["shapes"][name] = {"n_out": n, "k": k, "epilogue": epi, "ms": ms,
                                "tflops": flops / ms / 1e9,
                                "mfma_frac": flops / ms / 1e9 / PEAK_FP32_MFMA_TFLOPS}
+    # The same products without epilogues, beside the vendor library's fp32 GEMM (torch.mm,
+    # hipBLASLt / rocBLAS, TF32 off) on the same operands: a reference point, not a
+    # component of any line.
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        plain = {}
+        for name, n, k, epi in GEMM_SHAPES:
+            rows = 2 * n if epi == "geglu" else n
+            a, b = operands[name]
+            out = torch.empty(GEMM_M, rows, device="cuda")
+            ours = lambda a=a, b=b, out=out: g.matmul_nt_device(out, a, b, stream=stream)  # noqa: E731
+            vendor = lambda a=a, b=b, out=out: torch.mm(a, b.t(), out=out)  # noqa: E731
+            for _ in range(warmup):
+                ours()
+                vendor()
+            flops = 2.0 * GEMM_M * rows * k
+            # alternating, twice each, the faster of each pair
+            t = [timed(ours), timed(vendor), timed(ours), timed(vendor)]
+            t_ours, t_vendor = min(t[0], t[2]), min(t[1], t[3])
+            plain[f"{rows}x{k}"] = {"ms": t_ours, "tflops": flops / t_ours / 1e9,
+                                    "torch_mm_ms": t_vendor, "torch_mm_tflops": flops / t_vendor / 1e9}
+        res["plain_vs_torch_mm"] = plain
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
     return res
 
 
