@@ -147,6 +147,22 @@ def time_eager(step, steps: int, stream) -> tuple[float, float]:
     return e0.elapsed_time(e1) / 1e3 / steps, wall
 
 
+def time_per_launch(step, steps: int, stream) -> list[float]:
+    """Milliseconds of each of `steps` back-to-back launches: an event recorded on the launch
+    stream before every launch and one after the last (for launches much longer than the
+    host's launch path, so the stream never waits for the host)."""
+    import torch
+
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        ev[i].record(stream)
+        step()
+    ev[steps].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+
+
 def time_graph(launch_on, steps: int, stream) -> float:
     """Average seconds per launch over replays of a HIP graph holding GRAPH_LAUNCHES
     launches (captured on a side stream), one event pair around the replays."""
@@ -306,6 +322,12 @@ def attention_line(name: str, steps: int, warmup: int, cpu_seconds: float, cpu: 
         "kernel_ms": kern_s * 1e3,
         "timing": f"one event pair around {steps} back-to-back launches",
     }
+    if kern_s * 1e3 >= GRAPH_BELOW_MS:
+        per = sorted(time_per_launch(step, steps, stream))
+        line["per_launch_ms"] = {"median": statistics.median(per), "p10": per[len(per) // 10],
+                                 "p90": per[(9 * len(per)) // 10], "launches": len(per),
+                                 "timing": "an event pair per launch, a second run after the one above; "
+                                           "each launch also carries the marker between launches (~2 us)"}
     if kern_s * 1e3 < GRAPH_BELOW_MS:
         g_s = time_graph(launch_on, steps, stream)
         line["eager_kernel_ms"] = line["kernel_ms"]
