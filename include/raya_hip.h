@@ -215,7 +215,7 @@ int raya_matmul_nt_device(float *out, int64_t ldo, const float *a, int64_t lda, 
  * Attention uses the mask (mask_kind, mask_arg) and the per-sequence valid lengths, scale
  * 1/sqrt(head_dim); its rows at or beyond valid_len are zero, as Naive::attend's.  Weights are
  * device pointers in nn.Linear's [out_features][in_features] layout (wqkv: q, k and v stacked,
- * [3 hidden][hidden]); any bias may be NULL (zero).  LayerNorm eps is ln_eps. */
+ * [3 hidden][hidden]); any bias may be NULL (zero).  LayerNorm eps is ln_eps (finite, >= 0). */
 typedef struct raya_postln_layer {
     uint64_t batch, seq, hidden, heads, ffn;
     int32_t mask_kind;

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cinttypes>
+#include <cmath>
 
 #include "internal.hpp"
 #include "raya_hip.h"
@@ -63,6 +64,8 @@ int check_postln(const raya_postln_layer *L) {
     if (L->seq >= (uint64_t(1) << 30) || L->batch * L->seq > 0x7fffffffu || 3 * L->hidden > 0x3fffffffu ||
         L->ffn > 0x3fffffffu)
         return fail(RAYA_ERR_UNSUPPORTED, "unsupported: layer dimensions past the kernels' 32-bit indexing");
+    if (!(L->ln_eps >= 0.f) || !std::isfinite(L->ln_eps))
+        return fail(RAYA_ERR_SHAPE, "invalid shape: ln_eps must be finite and non-negative");
     if (!L->wqkv || !L->wo || !L->w1 || !L->w2 || !L->ln1_w || !L->ln2_w)
         return fail(RAYA_ERR_SHAPE, "invalid shape: null weight");
     return RAYA_OK;

@@ -46,6 +46,8 @@ class PostLNLayer:
                 raise ShapeError(f"invalid shape: `{name}` must be a contiguous {list(want[name])} tensor")
             if not t.is_cuda:
                 raise TypeError(f"`{name}` must be a torch tensor on the GPU")
+            if t.device != wqkv.device:
+                raise TypeError(f"`{name}` is on {t.device}, wqkv on {wqkv.device}")
             self.w[name] = t
         self.heads, self.eps = heads, eps
         self.mask = mask if mask is not None else Mask.block_diag(64)
@@ -68,6 +70,9 @@ class PostLNLayer:
                 or x.shape[2] != self.hidden or not x.is_contiguous():
             raise ShapeError(f"invalid shape: x must be a contiguous float32 [batch, seq, {self.hidden}] tensor")
         b, s, _ = x.shape
+        dev = self.w["wqkv"].device
+        if x.device != dev:
+            raise TypeError(f"x is on {x.device}, the layer's weights on {dev}")
         if not isinstance(valid_len, torch.Tensor) or valid_len.dtype != torch.int32 \
                 or valid_len.numel() != b or not valid_len.is_cuda:
             raise ShapeError("invalid shape: valid_len must be a GPU int32 tensor of batch entries")

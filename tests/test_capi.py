@@ -241,3 +241,13 @@ def test_postln_layer_checks_before_any_gpu_work():
     for name in ("wqkv", "wo", "w1", "w2", "ln1_w", "ln2_w"):
         setattr(odd, name, 256)
     assert lib.raya_postln_layer_forward(ctypes.byref(odd), 256, 256, 256, 256, 1 << 30, None) == C.RAYA_ERR_UNSUPPORTED
+
+
+def test_postln_layer_rejects_a_bad_eps():
+    lib = C.lib()
+    for eps in (-1e-5, float("nan"), float("inf")):
+        desc = C.PostLNLayerC(2, 16, 64, 2, 128, C.RAYA_MASK_BLOCKDIAG, 0, 16, eps)
+        for name in ("wqkv", "wo", "w1", "w2", "ln1_w", "ln2_w"):
+            setattr(desc, name, 256)
+        assert lib.raya_postln_workspace_bytes(ctypes.byref(desc)) == 0
+        assert "ln_eps" in C.last_error().message.decode()
