@@ -230,6 +230,11 @@ __device__ __forceinline__ int scatter(int i, int total, int half_bits) {
 // occupancy whose register budget holds the kernel without scratch spills.
 template <int DP>
 constexpr int kMinWaves = DP <= 64 ? 4 : DP == 128 ? 2 : 1;
+// The split kernel at head_dim 64 holds each tile's K/V subtile and the next one's in
+// registers: 3 waves per SIMD (768 workgroup slots, more than the small grids it serves
+// need at once).
+template <int DP, bool SPLIT, bool FUSED>
+constexpr int kMinWavesOf = SPLIT && FUSED ? 3 : kMinWaves<DP>;
 
 typedef __attribute__((address_space(3))) void lds_ptr_t;
 
@@ -485,6 +490,33 @@ __device__ __forceinline__ void pv_sub(const float *vs, const floatx4 &s, int g,
     }
 }
 
+// qk_sub and pv_sub with their operands already in registers (the split kernel's
+// direct path at head_dim 64).  The contraction index of MFMA step (c, e) in lane
+// group g is dim 16c + 4g + e here, so that the four lanes of a row read 64
+// contiguous bytes per load: k[c] holds dims 16c + 4g .. 16c + 4g + 3 of this lane's
+// Sᵀ key row and qreg[4c + e] the same dims of its query row; v[r] holds dims
+// 4li .. 4li + 3 of the subtile's key 4r + g.
+__device__ __forceinline__ floatx4 qk_regs(const float4 (&k)[4], const float (&qreg)[16]) {
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        acc = mfma(k[c].x, qreg[4 * c + 0], acc);
+        acc = mfma(k[c].y, qreg[4 * c + 1], acc);
+        acc = mfma(k[c].z, qreg[4 * c + 2], acc);
+        acc = mfma(k[c].w, qreg[4 * c + 3], acc);
+    }
+    return acc;
+}
+__device__ __forceinline__ void pv_regs(const float4 (&v)[4], const floatx4 &s, floatx4 (&oacc)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        oacc[0] = mfma(v[r].x, s[r], oacc[0]);
+        oacc[1] = mfma(v[r].y, s[r], oacc[1]);
+        oacc[2] = mfma(v[r].z, s[r], oacc[2]);
+        oacc[3] = mfma(v[r].w, s[r], oacc[3]);
+    }
+}
+
 // Stage clock of the instrumented kernel (raya_attend_batched_stages): the
 // shader clock (s_memtime) is read at each stage boundary of a tile and the
 // difference added to that stage's total.  The scheduling barriers keep the
@@ -539,6 +571,9 @@ __device__ __forceinline__ void lap(StageClock *c, uint64_t &bucket) {
 // fill the chip: a quarter of the MFMA chain per wave).  Each wave keeps its
 // own running max, sum and output over its keys; at the end the four partial
 // states are combined through LDS, each wave finishing a quarter of the dims.
+// At head_dim 64 (DIRECT) a wave's subtile of K and V goes straight into its
+// registers, since no other wave reads it: no LDS staging and no barrier
+// before the combine.
 template <int DP, bool FUSED, bool TIMED, bool SKIP = false, bool SPLIT = false>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs, StageClock *clk) {
@@ -548,6 +583,10 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     constexpr int NT = DP / 16;  // 16-dim output tiles
     constexpr int CH = DP / 4;   // 16-byte chunks per row
     constexpr int LPW = CH / kWaves;  // direct loads per wave per tile (each 64 chunks)
+    // SPLIT at head_dim 64: wave w only ever reads subtile w of each tile, so its K/V
+    // go straight into registers (no LDS staging, no barrier before the combine), the
+    // next tile's loaded while the current one is computed.
+    constexpr bool DIRECT = SPLIT && FUSED;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -674,7 +713,35 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         }
     };
     const int kt0 = tile_at(0);
-    if constexpr (FUSED) {
+    // Operand rows of this lane: S^T A-row i of subtile t is key 16t + 4(i%4) + i/4;
+    // the PV operand of (t, r) is row 16t + 4r + g, dims NT li .. NT li + NT.
+    const int k_row0 = 4 * (li & 3) + (li >> 2);
+    // The direct path's operands of tile kt: this wave's subtile, rows past the
+    // item's keys clamped to its last key.
+    const auto load_sub = [&](int kt, float4 (&kr)[4], float4 (&vr)[4]) {
+        const int key = min(kt + 16 * wave + k_row0, it.k_hi - 1);
+        const float *kp = kb + (int64_t)key * a.k_rs + 4 * g;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) kr[c] = *(const float4 *)(kp + 16 * c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int vkey = min(kt + 16 * wave + 4 * r + g, it.k_hi - 1);
+            vr[r] = *(const float4 *)(vb + (int64_t)vkey * a.v_rs + 4 * li);
+        }
+    };
+    float4 kcur[4], vcur[4];
+    if constexpr (DIRECT) {
+        const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)min(qi, valid - 1) * a.q_rs + 4 * g;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float4 x = *(const float4 *)(qp + 16 * c);
+            qreg[4 * c + 0] = x.x;
+            qreg[4 * c + 1] = x.y;
+            qreg[4 * c + 2] = x.z;
+            qreg[4 * c + 3] = x.w;
+        }
+        load_sub(kt0, kcur, vcur);
+    } else if constexpr (FUSED) {
         // K, Q and V in one asm block that ends waiting for K and Q only.
         const float *kbase, *vbase;
         uint32_t ko[4], kl[4], vo[4], vl[4];
@@ -709,16 +776,16 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     float m = -INFINITY;  // running max of raw dot products
     float l = 0.f;        // this lane's partial sum of weights
 
-    // Operand rows of this lane: S^T A-row i of subtile t is key 16t + 4(i%4) + i/4;
-    // the PV operand of (t, r) is row 16t + 4r + g, dims NT li .. NT li + NT.
-    const int k_row0 = 4 * (li & 3) + (li >> 2);
-
     if constexpr (TIMED) clk->last = clock_now();
     for (int j = 0; j < n_tiles; ++j) {
         const int kt = tile_at(j);
         int kx, ky;
         step_keys(kt, kx, ky);
-        if (j != 0) {
+        float4 knext[4], vnext[4];
+        if constexpr (DIRECT) {
+            if (j + 1 < n_tiles) load_sub(tile_at(j + 1), knext, vnext);
+        }
+        if (!DIRECT && j != 0) {
             // Every wave's LDS reads of the previous tile have returned.
             barrier_after_reads();
             if constexpr (FUSED) {
@@ -733,7 +800,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         }
         // This wave's K (and Q) loads have landed (the fused issue waited already) ...
         if constexpr (!FUSED) __builtin_amdgcn_s_waitcnt(kWaitAllButV);
-        barrier_only();  // ... and every other wave's
+        if constexpr (!DIRECT) barrier_only();  // ... and every other wave's
         if (j == 0) {
             // Q is zero on rows at or beyond valid and on dims at or beyond D; a
             // negative scale is carried by negating Q.
@@ -779,7 +846,9 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             if constexpr (SPLIT) clk->tiles += wave == 0 && rows_active;
         }
         if (active) {
-            if constexpr (SPLIT) {
+            if constexpr (DIRECT) {
+                ssub = qk_regs(kcur, qreg);
+            } else if constexpr (SPLIT) {
                 ssub = qk_sub<DP>(ks, qreg, g, k_row0, wave);
             } else {
                 qk_tile<DP>(ks, qreg, g, k_row0, sacc, live);
@@ -806,17 +875,30 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 lap(clk, clk->softmax);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's V loads have landed
-        barrier_only();
+        if constexpr (!DIRECT) {
+            __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's V loads have landed
+            barrier_only();
+        }
         if constexpr (TIMED) lap(clk, clk->load_wait);
         if (active) {
-            if constexpr (SPLIT)
+            if constexpr (DIRECT)
+                pv_regs(vcur, ssub, oacc);
+            else if constexpr (SPLIT)
                 pv_sub<DP>(vs, ssub, g, li, oacc, wave);
             else
                 pv_tile<DP>(vs, sacc, g, li, oacc, live);
             if constexpr (TIMED) {
                 settle(oacc);
                 lap(clk, clk->pv);
+            }
+        }
+        if constexpr (DIRECT) {
+            if (j + 1 < n_tiles) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    kcur[c] = knext[c];
+                    vcur[c] = vnext[c];
+                }
             }
         }
     }
@@ -914,7 +996,8 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel
 // 16-row items with the key tiles split over the four waves, for grids that
 // leave most compute units idle with 64-row items.
 template <int DP, bool FUSED>
-__global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_split_kernel(const AttnLaunch a, const Plan p) {
+__global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>)) attend_split_kernel(const AttnLaunch a,
+                                                                                               const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
     attend_body<DP, FUSED, false, false, true>(a, p, ks, vs, nullptr);
@@ -925,7 +1008,8 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_split_kernel(c
 // An item whose rows are all padding returns from the body in every wave with
 // zero totals.
 template <int DP, bool FUSED, bool SKIP, bool SPLIT = false>
-__global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_timed_kernel(const AttnLaunch a, const Plan p) {
+__global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, SPLIT, FUSED>)) attend_timed_kernel(const AttnLaunch a,
+                                                                                                const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
     __shared__ uint64_t part[kWaves][5];
