@@ -97,7 +97,11 @@ def host_cpu() -> dict:
 
 
 def cpu_threads() -> int:
-    return min(16, len(os.sched_getaffinity(0)))
+    """The CPU baselines' worker count: RAYA_THREADS, else the physical cores this process may
+    run on (the reference's default_threads, threads.rs:3-9)."""
+    from raya_amd import meta
+
+    return meta.default_threads()
 
 
 def kernel_mask(spec):

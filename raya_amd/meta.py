@@ -35,6 +35,35 @@ def label_for(target_env: str | None) -> str:
     return LABEL_UNLABELED
 
 
+def usable_physical_cores() -> int:
+    """Physical cores among the CPUs this process may run on (0 when the topology is not
+    readable)."""
+    cores = set()
+    for cpu in os.sched_getaffinity(0):
+        base = f"/sys/devices/system/cpu/cpu{cpu}/topology/"
+        try:
+            pkg = open(base + "physical_package_id").read().strip()
+            core = open(base + "core_id").read().strip()
+        except OSError:
+            return 0
+        cores.add((pkg, core))
+    return len(cores)
+
+
+def default_threads(env: str | None = None, *, use_env: bool = True) -> int:
+    """default_threads (crates/raya-kernels/src/threads.rs:3-9): RAYA_THREADS if it parses
+    to a positive integer (Rust's usize grammar: optional '+', decimal digits, surrounding
+    whitespace trimmed), else the physical cores this process may run on, at least 1."""
+    if env is None and use_env:
+        env = os.environ.get("RAYA_THREADS")
+    if env is not None:
+        t = env.strip()
+        digits = t[1:] if t.startswith("+") else t
+        if digits.isascii() and digits.isdigit() and int(digits) > 0:
+            return int(digits)
+    return max(1, usable_physical_cores() or len(os.sched_getaffinity(0)))
+
+
 def host_cpu() -> dict:
     """CPU model and core counts of this host."""
     model, cores = "unknown", set()

@@ -57,3 +57,23 @@ def test_build_stamp():
     assert b["commit"] == "unknown" or re.fullmatch(r"[0-9a-f]{40}", b["commit"])
     assert "--offload-arch=gfx950" in b["flags"] and "-packed-fp32-ops" in b["flags"]
     assert b["compiler"].startswith("HIP version") or b["compiler"] == "unknown"
+
+
+@pytest.mark.parametrize("value,want", [("4", 4), (" 8 ", 8), ("+3", 3), ("12\n", 12)])
+def test_raya_threads_parses_like_threads_rs(value, want):
+    """threads.rs:3-9: RAYA_THREADS when it parses to a positive usize."""
+    assert meta.default_threads(value) == want
+
+
+@pytest.mark.parametrize("value", ["0", "-2", "abc", "4.0", "1_000", "", "0x10", "٣"])
+def test_raya_threads_falls_back_to_physical_cores(value):
+    """Anything else (zero, signs, non-digits, Python-only integer spellings) falls back to the
+    physical cores this process may run on."""
+    assert meta.default_threads(value) == meta.default_threads(use_env=False) >= 1
+
+
+def test_raya_threads_env(monkeypatch):
+    monkeypatch.setenv("RAYA_THREADS", "5")
+    assert meta.default_threads() == 5
+    monkeypatch.delenv("RAYA_THREADS")
+    assert meta.default_threads() == meta.default_threads(use_env=False)
