@@ -1041,8 +1041,10 @@ int scatter_half_bits(int64_t total) {
 }
 
 // Grids of fewer 64-row items than this take the split kernel (16-row items,
-// each tile's keys split over the waves).
-constexpr int64_t kSplitBelow = 256;
+// each tile's keys split over the waves).  At 192 items the two kernels take
+// the same time; below, the split kernel is faster, above, the 64-row one (the
+// split kernel runs 3 workgroups per compute unit).
+constexpr int64_t kSplitBelow = 192;
 
 // RAYA_ATTN_ITEMS=16 or 64 forces the item height (as the reference's
 // RAYA_BACKEND forces a micro-kernel backend); anything else selects by grid.
