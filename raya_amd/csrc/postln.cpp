@@ -16,7 +16,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cinttypes>
+#include <climits>
 #include <cmath>
+#include <cstdint>
 
 #include "internal.hpp"
 #include "raya_hip.h"
@@ -61,9 +63,13 @@ int check_postln(const raya_postln_layer *L) {
         return fail(RAYA_ERR_UNSUPPORTED, "unsupported: mask kind %d", L->mask_kind);
     if (L->mask_kind == RAYA_MASK_BLOCKDIAG && L->mask_arg == 0)
         return fail(RAYA_ERR_SHAPE, "invalid shape: block_diag width must be at least 1");
-    if (L->seq >= (uint64_t(1) << 30) || L->batch * L->seq > 0x7fffffffu || 3 * L->hidden > 0x3fffffffu ||
-        L->ffn > 0x3fffffffu)
+    if (L->seq >= (uint64_t(1) << 30) || L->batch > 0x7fffffffu || L->batch * L->seq > 0x7fffffffu ||
+        3 * L->hidden > 0x3fffffffu || L->ffn > 0x3fffffffu)
         return fail(RAYA_ERR_UNSUPPORTED, "unsupported: layer dimensions past the kernels' 32-bit indexing");
+    // The workspace in bytes (6 hidden + ffn floats per token, plus 256-byte padding of
+    // its five parts) must fit 64 bits.
+    if (6 * L->hidden + L->ffn + 5 * 64 > (UINT64_MAX / sizeof(float)) / (L->batch * L->seq))
+        return fail(RAYA_ERR_UNSUPPORTED, "unsupported: a layer workspace past 64-bit sizes");
     if (!(L->ln_eps >= 0.f) || !std::isfinite(L->ln_eps))
         return fail(RAYA_ERR_SHAPE, "invalid shape: ln_eps must be finite and non-negative");
     if (!L->wqkv || !L->wo || !L->w1 || !L->w2 || !L->ln1_w || !L->ln2_w)

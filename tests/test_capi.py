@@ -251,3 +251,13 @@ def test_postln_layer_rejects_a_bad_eps():
             setattr(desc, name, 256)
         assert lib.raya_postln_workspace_bytes(ctypes.byref(desc)) == 0
         assert "ln_eps" in C.last_error().message.decode()
+
+
+def test_postln_layer_rejects_dimensions_past_its_indexing():
+    """A batch past 2^31 is rejected before batch x seq is formed (no wraparound)."""
+    lib = C.lib()
+    desc = C.PostLNLayerC(1 << 40, (1 << 30) - 1, 64, 2, 128, C.RAYA_MASK_BLOCKDIAG, 0, 16, 1e-5)
+    for name in ("wqkv", "wo", "w1", "w2", "ln1_w", "ln2_w"):
+        setattr(desc, name, 256)
+    assert lib.raya_postln_workspace_bytes(ctypes.byref(desc)) == 0
+    assert "32-bit indexing" in C.last_error().message.decode()
