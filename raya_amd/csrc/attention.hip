@@ -298,6 +298,12 @@ __device__ __forceinline__ void issue_kv64(const float *kbase, const uint32_t ko
 // themselves with explicit s_waitcnt; the clobber keeps the compiler from
 // moving memory operations across.
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
+// A non-temporal (streaming) 16-byte store: the output is not read again by this
+// launch, and whole lines written this way bypass the allocate-and-merge path.
+__device__ __forceinline__ void store_stream(float *p, float4 y) {
+    __builtin_nontemporal_store(floatx4{y.x, y.y, y.z, y.w}, (floatx4 *)p);
+}
 // A barrier after which other waves' direct loads overwrite LDS this wave has
 // read: its own LDS reads have returned first.
 __device__ __forceinline__ void barrier_after_reads() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -616,8 +622,14 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         if (packed) return;
         for (int c = tid; c < ROWS * CH; c += kThreads) {
             const int r = it.q0 + c / CH, c4 = c % CH;
-            if (r < a.seq && c4 < dch)
-                *(float4 *)(ob + (int64_t)r * a.o_rs + 4 * c4) = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < a.seq && c4 < dch) {
+                float *o = ob + (int64_t)r * a.o_rs + 4 * c4;
+                // At head_dim 64 a store instruction covers four whole 256-byte rows.
+                if constexpr (FUSED)
+                    store_stream(o, make_float4(0.f, 0.f, 0.f, 0.f));
+                else
+                    *(float4 *)o = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
         return;
     }
@@ -956,6 +968,39 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // beyond valid, and rows with no weight, are stored as literal zeros: their
     // accumulators are zero weights times V, which is NaN wherever V is not
     // finite.
+    if constexpr (FUSED) {
+        // The wave's 16 x 64 output block goes through its quarter of the K tile
+        // (no wave reads K after the last tile's V barrier) and leaves as whole
+        // rows: each store instruction writes four 256-byte rows, streamed past
+        // the caches.  In the accumulator layout a store covers 16-byte pieces
+        // 64 bytes apart, which only the L2 can merge into lines.  The row's
+        // 16-byte chunk c sits at chunk c ^ row, so both the writes (16 rows,
+        // one chunk each) and the reads (one row, 16 chunks) touch 16
+        // distinct chunk columns.
+        float *st = ks + wave * 16 * 64;
+        const bool zero_row = !(qi < valid && l > 0.f);
+        const float inv = zero_row ? 0.f : 1.f / l;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (!zero_row) {
+                y.x = oacc[0][c] * inv;
+                y.y = oacc[1][c] * inv;
+                y.z = oacc[2][c] * inv;
+                y.w = oacc[3][c] * inv;
+            }
+            *(float4 *)(st + li * 64 + 4 * ((4 * g + c) ^ li)) = y;
+        }
+        // One wave's LDS accesses complete in order: the reads see the writes.
+        const int rows = packed ? valid : a.seq;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int r = 4 * t + (lane >> 4), c = lane & 15;
+            const float4 y = *(const float4 *)(st + r * 64 + 4 * (c ^ r));
+            if (qw + r < rows) store_stream(ob + (int64_t)(qw + r) * a.o_rs + 4 * c, y);
+        }
+        return;
+    }
     if (qi < (packed ? valid : a.seq)) {
         const bool zero_row = !(qi < valid && l > 0.f);
         const float inv = zero_row ? 0.f : 1.f / l;
