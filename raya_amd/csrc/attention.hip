@@ -131,8 +131,10 @@ __device__ __forceinline__ int clamp_valid(const AttnLaunch &a, int b) {
 }
 
 // Item `item` of the (sequence, head, tile) order, tiles of ROWS query rows.
-template <int ROWS>
+// MK >= 0 fixes the mask kind at compile time (the launch has checked a.mask_kind).
+template <int ROWS, int MK = -1>
 __device__ __forceinline__ Item decode(const AttnLaunch &a, const Plan &p, int item) {
+    const int kind = MK >= 0 ? MK : a.mask_kind;
     Item it;
     const int bh = fdiv(item, p.by_qt);
     const int tile = item - bh * p.n_qt;
@@ -142,8 +144,8 @@ __device__ __forceinline__ Item decode(const AttnLaunch &a, const Plan &p, int i
     it.valid = clamp_valid(a, it.b);
     if (it.q0 < it.valid) {
         const int qlast = min(it.q0 + ROWS, it.valid) - 1;
-        it.k_lo = key_range(a.mask_kind, a.mask_arg, p.by_arg, it.q0, it.valid).lo;
-        it.k_hi = key_range(a.mask_kind, a.mask_arg, p.by_arg, qlast, it.valid).hi;
+        it.k_lo = key_range(kind, a.mask_arg, p.by_arg, it.q0, it.valid).lo;
+        it.k_hi = key_range(kind, a.mask_arg, p.by_arg, qlast, it.valid).hi;
     } else {
         it.k_lo = it.k_hi = 0;
     }
@@ -580,7 +582,10 @@ __device__ __forceinline__ void lap(StageClock *c, uint64_t &bucket) {
 // At head_dim 64 (DIRECT) a wave's subtile of K and V goes straight into its
 // registers, since no other wave reads it: no LDS staging and no barrier
 // before the combine.
-template <int DP, bool FUSED, bool TIMED, bool SKIP = false, bool SPLIT = false>  // head_dim padded to a multiple of 16
+// MK >= 0: the mask kind is fixed at compile time; SINGLE: every item's keys fit one
+// tile (BlockDiag(b) with b dividing 64).  Both only drop code the launch has ruled out.
+template <int DP, bool FUSED, bool TIMED, bool SKIP = false, bool SPLIT = false, int MK = -1,
+          bool SINGLE = false>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs, StageClock *clk) {
     static_assert(!FUSED || DP == 64, "the fused issue is written for head_dim 64");
@@ -601,7 +606,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     const int li = lane & 15;
     const int D = a.head_dim;
     const int dch = D / 4;  // valid chunks per row
-    const int kind = a.mask_kind, arg = a.mask_arg;
+    const int kind = MK >= 0 ? MK : a.mask_kind, arg = a.mask_arg;
     // exp(scale * (x - y)) = exp2((x - y) * c) on raw dot products x, y; a
     // negative scale is carried by negating Q, so c > 0 and max commutes.  c is
     // kept at least FLT_MIN so that a masked key (x = -inf) weighs exactly 0
@@ -610,7 +615,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     const float c_exp = fmaxf(fabsf(a.scale) * kLog2e, 1.17549435e-38f);
     const float q_sign = a.scale < 0.f ? -1.f : 1.f;
 
-    const Item it = decode<ROWS>(a, p, item_of(blockIdx.x, p));
+    const Item it = decode<ROWS, MK>(a, p, item_of(blockIdx.x, p));
     // Packed sequences start at a row offset and have no padded rows in memory.
     const bool packed = a.seq_start != nullptr;
     const int64_t row0 = packed ? (int64_t)a.seq_start[it.b] : 0;
@@ -697,7 +702,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // of a tile, which go to HBM, spread over all n steps instead of all landing
     // in the first, and overlap the other steps' arithmetic.  The softmax is
     // independent of the order.
-    const int n_tiles = (it.k_hi - it.k_lo + kKeys - 1) / kKeys;
+    const int n_tiles = SINGLE ? 1 : (it.k_hi - it.k_lo + kKeys - 1) / kKeys;
     int rot = 0;
     if (n_tiles > 1) {
         rot = (it.k_lo / kKeys) % n_tiles;
@@ -1031,6 +1036,18 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_kernel(const A
 // Head_dim 64 under Window64 and Sliding(w): the fused kernel with subtile
 // skipping (+7% on Window64 at L = 8192; no use for the block masks, whose
 // items' key ranges cover whole subtiles).
+// BlockDiag(b) with b dividing 64 at head_dim 64: every item is one 64-key tile,
+// and the mask is known, so the item decode and key ranges compile to a few
+// scalar instructions (the general kernel's first K/V load sits behind the
+// decode of every mask kind and the tile walk's set-up): 64 VGPRs instead of
+// 126, and the first load about 420 instructions earlier.
+template <int DP>
+__global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_blockdiag_kernel(const AttnLaunch a, const Plan p) {
+    __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
+    __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
+    attend_body<DP, true, false, false, false, RAYA_MASK_BLOCKDIAG, true>(a, p, ks, vs, nullptr);
+}
+
 template <int DP>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
@@ -1135,6 +1152,8 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
             hipLaunchKernelGGL((attend_timed_kernel<DP, true, false>), grid, block, 0, stream, a, p);
         else if (sliding)
             hipLaunchKernelGGL((attend_sliding_kernel<DP>), grid, block, 0, stream, a, p);
+        else if (a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
+            hipLaunchKernelGGL((attend_blockdiag_kernel<DP>), grid, block, 0, stream, a, p);
         else
             hipLaunchKernelGGL((attend_kernel<DP, true>), grid, block, 0, stream, a, p);
     } else {
