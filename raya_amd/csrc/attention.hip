@@ -758,6 +758,9 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             qreg[4 * c + 3] = x.w;
         }
         load_sub(kt0, kcur, vcur);
+        // A single tile's loads all leave here: the scheduler would otherwise sink each
+        // one next to its first use and wait for it alone.
+        if constexpr (SINGLE) __builtin_amdgcn_sched_barrier(0);
     } else if constexpr (FUSED) {
         // K, Q and V in one asm block that ends waiting for K and Q only.
         const float *kbase, *vbase;
@@ -1057,12 +1060,13 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel
 
 // 16-row items with the key tiles split over the four waves, for grids that
 // leave most compute units idle with 64-row items.
-template <int DP, bool FUSED>
-__global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>)) attend_split_kernel(const AttnLaunch a,
-                                                                                               const Plan p) {
+template <int DP, bool FUSED, int MK = -1, bool SINGLE = false>
+__global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>))
+__attribute__((amdgpu_waves_per_eu(1, kMinWavesOf<DP, true, FUSED>))) attend_split_kernel(const AttnLaunch a,
+                                                                                           const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, FUSED, false, false, true>(a, p, ks, vs, nullptr);
+    attend_body<DP, FUSED, false, false, true, MK, SINGLE>(a, p, ks, vs, nullptr);
 }
 
 // The same kernel with the stage clock.  Per-wave totals are summed in LDS,
@@ -1141,6 +1145,8 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     if (split) {
         if (a.stage_cycles)
             hipLaunchKernelGGL((attend_timed_kernel<DP, FUSED, false, true>), grid, block, 0, stream, a, p);
+        else if (FUSED && a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
+            hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, RAYA_MASK_BLOCKDIAG, true>), grid, block, 0, stream, a, p);
         else
             hipLaunchKernelGGL((attend_split_kernel<DP, FUSED>), grid, block, 0, stream, a, p);
         return hipGetLastError();
