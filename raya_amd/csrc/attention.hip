@@ -1061,9 +1061,8 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel
 // 16-row items with the key tiles split over the four waves, for grids that
 // leave most compute units idle with 64-row items.
 template <int DP, bool FUSED, int MK = -1, bool SINGLE = false>
-__global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>))
-__attribute__((amdgpu_waves_per_eu(1, kMinWavesOf<DP, true, FUSED>))) attend_split_kernel(const AttnLaunch a,
-                                                                                           const Plan p) {
+__global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>)) attend_split_kernel(const AttnLaunch a,
+                                                                                               const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
     attend_body<DP, FUSED, false, false, true, MK, SINGLE>(a, p, ks, vs, nullptr);
