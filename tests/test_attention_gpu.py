@@ -190,6 +190,39 @@ def test_batched_device_path_dense_and_strided(hip_attention):
         check_close(ctx.cpu().numpy().transpose(0, 2, 1, 3), want, f"strided {name}")
 
 
+@pytest.mark.parametrize("width", [1, 2, 4, 8, 16, 32, 64, 48, 96])
+def test_block_diag_widths_dense_and_strided(hip_attention, width):
+    """BlockDiag(b) at head_dim 64 for every b dividing 64 (the single-tile kernels, mask
+    kind fixed at compile time) and two widths that do not (items meeting two tiles), over
+    padded sequences, dense and packed layouts; the seq length 200 leaves a partial block
+    and a partial 64-row item at the end."""
+    b, h, s, d = 3, 2, 200, 64
+    valid = np.array([200, 131, 0], np.int32)
+    q, k, v = (synth.normal(40 + i, b * h * s * d).reshape(b, h, s, d) for i in range(3))
+    mask = R.Mask.block_diag(width)
+    want = oracle.naive_attend_batched(q, k, v, oracle.MASK_BLOCKDIAG, valid, R.kernels.default_scale(d),
+                                       block=width)
+    out = torch.full((b, h, s, d), float("nan"), device="cuda")
+    hip_attention.attend_batched(_dev(q), _dev(k), _dev(v), out, _dev(valid), mask)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    check_close(got, want, f"dense block_diag({width})")
+    for i in range(b):
+        assert (got[i, :, valid[i]:, :] == 0).all()
+    packed = np.stack([q, k, v], axis=2).transpose(0, 3, 2, 1, 4).copy()  # b, s, 3, h, d
+    pk = _dev(packed)
+    ctx = torch.full((b, s, h, d), float("nan"), device="cuda")
+    qkv_lay = (s * 3 * h * d, d, 3 * h * d)
+    lay = {"shape": (b, h, s, d), "q": qkv_lay, "k": qkv_lay, "v": qkv_lay, "out": (s * h * d, d, h * d)}
+    hip_attention.attend_batched(pk[:, :, 0], pk[:, :, 1], pk[:, :, 2], ctx, _dev(valid), mask, layouts=lay)
+    torch.cuda.synchronize()
+    check_close(ctx.cpu().numpy().transpose(0, 2, 1, 3), want, f"strided block_diag({width})")
+    if width == 1:
+        # Each query sees only its own key: weight exactly 1, so the output is V itself.
+        for i in range(b):
+            assert (got[i, :, : valid[i]] == v[i, :, : valid[i]]).all()
+
+
 def test_workload_block_diag64_b1_l512(hip_attention):
     """B=1, H=12, D=64, L=512, BlockDiag(64), N(0,1) inputs, no padding."""
     h, s, d = 12, 512, 64
