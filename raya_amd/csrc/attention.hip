@@ -1051,11 +1051,11 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_blockdiag_kern
     attend_body<DP, true, false, false, false, RAYA_MASK_BLOCKDIAG, true>(a, p, ks, vs, nullptr);
 }
 
-template <int DP>
+template <int DP, int MK>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, true, false, true>(a, p, ks, vs, nullptr);
+    attend_body<DP, true, false, true, false, MK>(a, p, ks, vs, nullptr);
 }
 
 // 16-row items with the key tiles split over the four waves, for grids that
@@ -1155,8 +1155,10 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
             hipLaunchKernelGGL((attend_timed_kernel<DP, true, true>), grid, block, 0, stream, a, p);
         else if (a.stage_cycles)
             hipLaunchKernelGGL((attend_timed_kernel<DP, true, false>), grid, block, 0, stream, a, p);
+        else if (a.mask_kind == RAYA_MASK_WINDOW64)
+            hipLaunchKernelGGL((attend_sliding_kernel<DP, RAYA_MASK_WINDOW64>), grid, block, 0, stream, a, p);
         else if (sliding)
-            hipLaunchKernelGGL((attend_sliding_kernel<DP>), grid, block, 0, stream, a, p);
+            hipLaunchKernelGGL((attend_sliding_kernel<DP, RAYA_MASK_SLIDING>), grid, block, 0, stream, a, p);
         else if (a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
             hipLaunchKernelGGL((attend_blockdiag_kernel<DP>), grid, block, 0, stream, a, p);
         else
