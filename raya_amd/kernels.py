@@ -220,6 +220,24 @@ def _dev_ptr(t, name: str) -> ctypes.c_void_p:
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _layout_reach(strides, b: int, h: int, s: int, d: int) -> int:
+    """One past the last float a [b, h, s, d] operand with (batch, head, row)
+    strides touches (all zero: the dense layout).  Negative strides are left
+    to the library, which rejects them."""
+    bs, hs, rs = strides
+    if bs == 0 and hs == 0 and rs == 0:
+        return b * h * s * d
+    if min(b, h, s, d) <= 0 or min(bs, hs, rs) < 0:
+        return 0
+    return (b - 1) * bs + (h - 1) * hs + (s - 1) * rs + d
+
+
+def _floats_from(t) -> int:
+    """Floats between a tensor's pointer and the end of its storage."""
+    st = t.untyped_storage()
+    return (st.nbytes() - (t.data_ptr() - st.data_ptr())) // 4
+
+
 def _stream_ptr(stream) -> ctypes.c_void_p:
     import torch
 
@@ -286,6 +304,14 @@ class HipAttention(AttentionKernel):
         else:
             b, h, s_, d = layouts["shape"]
             lay = {n: layouts[n] for n in ("q", "k", "v", "out")}
+            # The library sees bare pointers: every element a layout reaches must lie
+            # inside the tensor's storage, counted from the tensor's own pointer.
+            for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+                reach = _layout_reach(lay[name], b, h, s_, d)
+                have = _floats_from(t)
+                if reach > have:
+                    raise ShapeError(f"invalid shape: the layout of `{name}` reaches {reach} floats past its "
+                                     f"pointer, which holds {have}")
         for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
             if t.dtype != torch.float32:
                 raise TypeError(f"`{name}` must be float32")

@@ -224,6 +224,32 @@ def test_gemm_device_arguments_are_checked_before_any_launch():
         g.matmul_nt_device(out, a, b, bias=torch.zeros(n), residual=torch.zeros(m, n))
 
 
+def test_attend_batched_layouts_must_stay_inside_their_tensors():
+    """With explicit strides, a layout that reaches past a tensor's storage is a Shape
+    error before any pointer reaches the library; one that fits gets past that check
+    (here to the host-tensor check that follows it)."""
+    import torch
+
+    att = R.HipAttention()
+    b, h, s, d = 2, 3, 5, 8
+    # q, k, v interleaved per row as in a packed QKV projection: [b, s, 3, h, d].
+    qkv = torch.zeros(b, s, 3, h, d)
+    out = torch.zeros(b, h, s, d)
+    strided = (s * 3 * h * d, d, 3 * h * d)
+    lay = {"shape": (b, h, s, d), "q": strided, "k": strided, "v": strided, "out": (0, 0, 0)}
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    valid = torch.full((b,), s, dtype=torch.int32)
+    with pytest.raises(R.ShapeError, match="valid_len"):  # fits: stops at the GPU checks
+        att.attend_batched(q, k, v, out, valid, R.Mask.BLOCK3, layouts=lay)
+    too_far = dict(lay, v=(s * 3 * h * d + 4, d, 3 * h * d))  # batch stride one chunk too long
+    with pytest.raises(R.ShapeError, match="layout of `v`"):
+        att.attend_batched(q, k, v, out, valid, R.Mask.BLOCK3, layouts=too_far)
+    with pytest.raises(R.ShapeError, match="layout of `out`"):  # dense out one row short
+        att.attend_batched(q, k, v, torch.zeros(b * h * s * d - d), valid, R.Mask.BLOCK3, layouts=lay)
+    with pytest.raises(R.ShapeError, match="layout of `q`"):  # a longer shape than the buffer holds
+        att.attend_batched(q, k, v, out, valid, R.Mask.BLOCK3, layouts=dict(lay, shape=(b, h, s + 1, d)))
+
+
 def test_postln_layer_checks_before_any_gpu_work():
     """The post-LN layer rejects bad shapes and a short workspace without touching the GPU."""
     lib = C.lib()
