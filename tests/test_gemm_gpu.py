@@ -201,3 +201,42 @@ def test_random_sweep_of_shapes_and_epilogues(hip_gemm):
         tol = 2 * err + 1e-6 * (1 + np.abs(want))
         assert (diff <= tol).all(), (case, float((diff - tol).max()))
         assert (got[:, n:] == 9.0).all()
+
+
+@pytest.mark.parametrize("shape", ["qkv", "wo", "geglu", "mlp_wo"])
+def test_encoder_shapes_at_the_forward_row_count(hip_gemm, shape):
+    """The four encoder projections at the measured forward's M = 21,405 packed tokens
+    (167 whole 128-row tiles and a last one of 29 rows), with the epilogue each takes in the
+    forward.  Every output element is held to the reordering bound around a float64 product
+    computed on the device (the bound is what the sequential fp32 result itself meets), carried
+    through GeGLU as in the sweep above.  The residual shapes pass `out` as their own residual,
+    as the forward does."""
+    m = 21405
+    n, k, act, residual = {"qkv": (2304, 768, C.RAYA_EPI_NONE, False), "wo": (768, 768, C.RAYA_EPI_NONE, True),
+                           "geglu": (3072, 768, C.RAYA_EPI_GEGLU, False),
+                           "mlp_wo": (768, 3072, C.RAYA_EPI_NONE, True)}[shape]
+    rows_b = 2 * n if act == C.RAYA_EPI_GEGLU else n
+    gen = torch.Generator(device="cuda").manual_seed(2024)
+    a = torch.randn(m, k, device="cuda", generator=gen)
+    b = 0.02 * torch.randn(rows_b, k, device="cuda", generator=gen)
+    res = torch.randn(m, n, device="cuda", generator=gen) if residual else None
+    out = res.clone() if residual else torch.full((m, n), 9.0, device="cuda")
+    hip_gemm.matmul_nt_device(out, a, b, activation=act, residual=out if residual else None)
+    torch.cuda.synchronize()
+    a64, b64 = a.double(), b.double()
+    y = a64 @ b64.T
+    err = 2 * k * 2.0 ** -24 * (a64.abs() @ b64.abs().T)
+    if act == C.RAYA_EPI_GEGLU:
+        x, g = y[:, :n], y[:, n:]
+        gx = torch.nn.functional.gelu(x)  # exact erf form, float64
+        want = gx * g
+        err = 1.13 * err[:, :n] * g.abs() + gx.abs() * err[:, n:] + 1e-6 * want.abs()
+    else:
+        want = y
+    if residual:
+        want = want + res.double()
+    diff = (out.double() - want).abs()
+    tol = err + 1e-6 * (1 + want.abs())
+    worst = float((diff - tol).max())
+    print(f"{shape}: max |diff| {float(diff.max()):.3g}, worst margin {worst:.3g}")
+    assert worst <= 0, worst
