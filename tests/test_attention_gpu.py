@@ -346,6 +346,36 @@ def test_full_size_properties_b32_l2048(hip_attention):
     assert bool(torch.all(torch.where(rows, True, o12 == 0)))
 
 
+def test_full_size_b32_l2048_against_float64(hip_attention):
+    """The whole measured batch shape (B=32 x 12 x 2048, head_dim 64, BlockDiag(64), the
+    workload's own valid lengths; N(0,1) inputs drawn on the device): every valid element
+    against a float64 evaluation on the device within max-abs 1e-5 and rel-L2 1e-6, every
+    padded row exactly zero (the output starts as NaN, so no element may be left unwritten)."""
+    b, h, s, d = 32, 12, 2048, 64
+    g = torch.Generator(device="cuda").manual_seed(99)
+    q, k, v = (torch.randn((b, h, s, d), device="cuda", generator=g) for _ in range(3))
+    valid_np = synth.integers(synth.workload_seed(2, 3), b, s // 4, s).astype(np.int32)
+    valid = _dev(valid_np)
+    out = torch.full((b, h, s, d), float("nan"), device="cuda")
+    hip_attention.attend_batched(q, k, v, out, valid, R.Mask.block_diag(64))
+    torch.cuda.synchronize()
+    nb = s // 64
+    q64, k64, v64 = (x.double().view(b, h, nb, 64, d) for x in (q, k, v))
+    sc = torch.matmul(q64, k64.transpose(-1, -2).contiguous()) * 0.125  # [b, h, block, row, key]
+    key = torch.arange(s, device="cuda").view(1, 1, nb, 1, 64)
+    sc = sc.masked_fill(key >= valid.long().view(b, 1, 1, 1, 1), float("-inf"))
+    want = torch.matmul(torch.softmax(sc, dim=-1), v64).view(b, h, s, d)
+    del q64, k64, v64, sc
+    rows = torch.arange(s, device="cuda").view(1, 1, s, 1) < valid.long().view(b, 1, 1, 1)
+    assert bool(torch.all(torch.where(rows, True, out == 0)))
+    diff = torch.where(rows, out.double() - want, 0.0)
+    ref = torch.where(rows, want, 0.0)
+    max_abs = float(diff.abs().max())
+    rel = float(diff.norm() / ref.norm())
+    print(f"max-abs {max_abs:.3g}, rel-L2 {rel:.3g} against float64")
+    assert max_abs < 1e-5 and rel < 1e-6
+
+
 def test_random_sweep_against_the_oracle(hip_attention):
     """48 random batched launches against the oracle: batch 1-4, heads 1-3, seq 1-700,
     every head_dim multiple of 8 up to 128, every mask with random widths (BlockDiag(b) and
