@@ -376,6 +376,41 @@ def test_full_size_b32_l2048_against_float64(hip_attention):
     assert max_abs < 1e-5 and rel < 1e-6
 
 
+def test_full_size_block3_b32_l2048_against_float64(hip_attention):
+    """The reference's own Block3 mask (a row's 128-block and both neighbours) at the same
+    full batch: every valid element against a float64 evaluation on the device that gathers
+    each block's three key blocks, max-abs 1e-5 and rel-L2 1e-6; padded rows exactly zero."""
+    b, h, s, d, blk = 32, 12, 2048, 64, 128
+    g = torch.Generator(device="cuda").manual_seed(98)
+    q, k, v = (torch.randn((b, h, s, d), device="cuda", generator=g) for _ in range(3))
+    valid_np = synth.integers(synth.workload_seed(2, 3), b, s // 4, s).astype(np.int32)
+    valid = _dev(valid_np)
+    out = torch.full((b, h, s, d), float("nan"), device="cuda")
+    hip_attention.attend_batched(q, k, v, out, valid, R.Mask.BLOCK3)
+    torch.cuda.synchronize()
+    nb = s // blk
+    zero = torch.zeros((b, h, blk, d), device="cuda", dtype=torch.float64)
+
+    def three_blocks(x):  # [b, h, nb, 3 * blk, d]: blocks i - 1, i, i + 1 (zeros past the ends)
+        xp = torch.cat([zero, x.double(), zero], dim=2).view(b, h, nb + 2, blk, d)
+        return torch.cat([xp[:, :, :-2], xp[:, :, 1:-1], xp[:, :, 2:]], dim=3)
+
+    k3, v3 = three_blocks(k), three_blocks(v)
+    q64 = q.double().view(b, h, nb, blk, d)
+    sc = torch.matmul(q64, k3.transpose(-1, -2).contiguous()) * 0.125  # [b, h, block, row, 3 blk]
+    key = (torch.arange(nb, device="cuda").view(nb, 1) - 1) * blk + torch.arange(3 * blk, device="cuda")
+    dead = (key < 0).view(1, 1, nb, 1, 3 * blk) | (key.view(1, 1, nb, 1, 3 * blk) >= valid.long().view(b, 1, 1, 1, 1))
+    want = torch.matmul(torch.softmax(sc.masked_fill(dead, float("-inf")), dim=-1), v3).view(b, h, s, d)
+    del k3, v3, q64, sc
+    rows = torch.arange(s, device="cuda").view(1, 1, s, 1) < valid.long().view(b, 1, 1, 1)
+    assert bool(torch.all(torch.where(rows, True, out == 0)))
+    diff = torch.where(rows, out.double() - want, 0.0)
+    max_abs = float(diff.abs().max())
+    rel = float(diff.norm() / torch.where(rows, want, 0.0).norm())
+    print(f"max-abs {max_abs:.3g}, rel-L2 {rel:.3g} against float64")
+    assert max_abs < 1e-5 and rel < 1e-6
+
+
 def test_random_sweep_against_the_oracle(hip_attention):
     """48 random batched launches against the oracle: batch 1-4, heads 1-3, seq 1-700,
     every head_dim multiple of 8 up to 128, every mask with random widths (BlockDiag(b) and
