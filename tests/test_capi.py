@@ -287,3 +287,10 @@ def test_postln_layer_rejects_dimensions_past_its_indexing():
         setattr(desc, name, 256)
     assert lib.raya_postln_workspace_bytes(ctypes.byref(desc)) == 0
     assert "32-bit indexing" in C.last_error().message.decode()
+
+
+def test_integration_notes_bind_every_declared_function():
+    """The Rust binding in INTEGRATION.md declares every function include/*.h exports."""
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    missing = [n for n in declared_functions() if not re.search(r"pub fn " + n + r"\(", doc)]
+    assert not missing, missing
