@@ -319,6 +319,47 @@ def test_workload_block_diag128_l16384_outliers(hip_attention):
           f"rms hip {rms_hip:.3g}, naive {rms_naive:.3g}; rel-L2 vs naive {rel:.3g}")
 
 
+def test_block_diag128_l16384_outliers_whole_batch(hip_attention):
+    """The whole B=4 batch of the L=16384 BlockDiag(128) workload shape (the workload's valid
+    lengths, N(0,1) inputs with 1% of entries x20, drawn on the device): every valid element
+    within the same forward-error bound around a float64 evaluation as the one-sequence test
+    above, computed on the device block by block; padded rows exactly zero."""
+    b, h, s, d, blk = 4, 12, 16384, 64, 128
+    scale, eps = 0.125, 2.0 ** -24
+    g = torch.Generator(device="cuda").manual_seed(55)
+
+    def draw():
+        x = torch.randn((b, h, s, d), device="cuda", generator=g)
+        hit = torch.rand((b, h, s, d), device="cuda", generator=g) < 0.01
+        return torch.where(hit, 20.0 * x, x)
+
+    q, k, v = draw(), draw(), draw()
+    valid_np = synth.integers(synth.workload_seed(5, 3), b, s // 2, s).astype(np.int32)
+    out = torch.full((b, h, s, d), float("nan"), device="cuda")
+    hip_attention.attend_batched(q, k, v, out, _dev(valid_np), R.Mask.block_diag(blk))
+    torch.cuda.synchronize()
+    worst = torch.zeros((), dtype=torch.float64, device="cuda")
+    for i in range(b):
+        n = int(valid_np[i])
+        assert bool(torch.all(out[i, :, n:] == 0))
+        for c0 in range(0, n, blk):
+            c1 = min(c0 + blk, n)
+            q64, k64, v64 = (x[i, :, c0:c1].double() for x in (q, k, v))
+            sc = torch.matmul(q64, k64.transpose(1, 2).contiguous()) * scale
+            m = sc.amax(-1, keepdim=True)
+            p = torch.softmax(sc, dim=-1)
+            o = torch.matmul(p, v64)
+            ds = 2 * d * eps * scale * torch.matmul(q64.abs(), k64.abs().transpose(1, 2).contiguous())
+            ds += 4 * eps * (1 + (sc - m).abs())
+            dev = (v64[:, None, :, :] - o[:, :, None, :]).abs()  # [h, i, j, c]
+            bound = torch.einsum("hij,hijc->hic", p * ds, dev)
+            bound += 2 * (c1 - c0 + 4) * eps * torch.matmul(p, v64.abs())
+            worst = torch.maximum(worst, ((out[i, :, c0:c1].double() - o).abs() / bound).max())
+    worst = float(worst)
+    print(f"worst error / bound {worst:.3g}")
+    assert worst <= 1.0, worst
+
+
 def test_full_size_properties_b32_l2048(hip_attention):
     """At the full B=32 workload: with V = 1 every valid row is exactly a convex combination
     summing to 1; linearity in V holds; padded rows are zero."""
