@@ -3,7 +3,8 @@ which tests/test_oracle_postln.py pins to torch's nn.TransformerEncoderLayer in 
 
 * The configuration itself: 16 sequences of 1024 tokens, hidden 768 = 12 x 64, GELU 3072,
   eps 1e-12, N(0, 0.02) weights, zero biases, gain 1 and shift 0, N(0, 1) inputs,
-  BlockDiag(64); sequences 0 and 15 through the oracle at max-abs 1e-4 and rel-L2 1e-5.
+  BlockDiag(64); sequences 0 and 15 through the oracle at max-abs 1e-4 and rel-L2 1e-5, and
+  the whole batch against torch's float64 layer on the device at the same bars.
 * Smaller layers with random biases, gains and shifts, padding and the other masks, head dims
   32 and 64, at max-abs 1e-5 on the valid rows."""
 import numpy as np
@@ -70,3 +71,43 @@ def test_small_layers_with_biases_match_the_oracle(d, heads, ffn, seq, valids, m
         want = F.postln_layer(x[i], v, w, heads, 1e-5, kind, arg)
         err = float(np.abs(out[i, :v] - want[:v]).max())
         assert err <= 1e-5, (i, err)
+
+
+@pytest.mark.timeout(600)
+def test_the_postln_workload_whole_batch_against_torch_float64():
+    """Every token of all 16 sequences of the measured configuration against torch's own
+    nn.TransformerEncoderLayer(norm_first=False, activation="gelu") evaluated in float64 on
+    the device with the same weights and a BlockDiag(64) attention mask: max-abs 1e-4 and
+    rel-L2 1e-5 over the whole batch."""
+    spec = W.POSTLN_LAYER
+    x, valid, w = W.postln_inputs(spec)
+    b, s, d = x.shape
+    layer = PostLNLayer({k: dev(v) for k, v in w.items()}, spec["heads"], spec["eps"], Mask.block_diag(spec["block"]))
+    out = layer.forward(dev(x), dev(valid)).double()
+    ref = torch.nn.TransformerEncoderLayer(d, spec["heads"], dim_feedforward=spec["ffn"], dropout=0.0,
+                                           activation="gelu", layer_norm_eps=spec["eps"], batch_first=True,
+                                           norm_first=False, dtype=torch.float64, device="cuda")
+    t = lambda a: dev(np.asarray(a, np.float64))  # noqa: E731
+    with torch.no_grad():
+        ref.self_attn.in_proj_weight.copy_(t(w["wqkv"]))
+        ref.self_attn.in_proj_bias.copy_(t(w["bqkv"]))
+        ref.self_attn.out_proj.weight.copy_(t(w["wo"]))
+        ref.self_attn.out_proj.bias.copy_(t(w["bo"]))
+        ref.linear1.weight.copy_(t(w["w1"]))
+        ref.linear1.bias.copy_(t(w["b1"]))
+        ref.linear2.weight.copy_(t(w["w2"]))
+        ref.linear2.bias.copy_(t(w["b2"]))
+        ref.norm1.weight.copy_(t(w["ln1_w"]))
+        ref.norm1.bias.copy_(t(w["ln1_b"]))
+        ref.norm2.weight.copy_(t(w["ln2_w"]))
+        ref.norm2.bias.copy_(t(w["ln2_b"]))
+        ref.train()  # dropout is 0; train mode keeps the plain (non-fused) path
+        i = torch.arange(s, device="cuda")
+        blocks = (i[:, None] // spec["block"]) == (i[None, :] // spec["block"])
+        mask = torch.zeros(s, s, dtype=torch.float64, device="cuda").masked_fill(~blocks, float("-inf"))
+        assert bool((torch.from_numpy(valid) == s).all())  # the configuration has no padding
+        want = torch.cat([ref(t(x[j:j + 4]), src_mask=mask) for j in range(0, b, 4)])
+    diff = out - want
+    err, rel = float(diff.abs().max()), float(diff.norm() / want.norm())
+    print(f"whole batch: max-abs {err:.2e} rel-L2 {rel:.2e}", flush=True)
+    assert err <= 1e-4 and rel <= 1e-5, (err, rel)
