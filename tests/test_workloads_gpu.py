@@ -124,3 +124,31 @@ def test_twelve_layer_encoder_workload(tmp_path):
         print(f"  sequence {i} (valid {v}) done", flush=True)
     print({k: f"{a:.1e}/{r:.1e}" for k, (a, r) in worst.items()}, flush=True)
     assert {f"encoder_layer_{i:02d}" for i in range(12)} <= set(worst)
+
+
+@pytest.mark.timeout(600)
+def test_twelve_layer_encoder_batch_order_and_size(tmp_path):
+    """Whole-batch properties of the bench's 12-layer forward (all 64 sequences): reversing
+    the batch reverses every output bit for bit (each sequence's rows, tiles and statistics
+    are computed the same wherever it sits in the packed batch, so nothing leaks between
+    sequences); and each group of 8 sequences run on its own (a smaller grid, where the
+    attention may take its other kernel) agrees with the batch of 64 at the fp32 bar."""
+    spec = W.ENCODER
+    ckpt = str(tmp_path / "enc")
+    checkpoint.write_synthetic(ckpt, seed=W.ENCODER_WEIGHT_SEED)
+    model = M.Model.load(ckpt)
+    ids, valid, pos, mask, qtype = W.encoder_inputs(spec)
+    fields = ("logits", "probabilities", "act_logits", "features", "pooled")
+    out = model.forward_batch(ids, valid, pos, mask, qtype)
+    rev = slice(None, None, -1)
+    back = model.forward_batch(ids[rev], valid[rev], pos[rev], mask[rev], qtype[rev])
+    for f in fields:
+        assert np.array_equal(getattr(back, f)[rev], getattr(out, f)), f
+    worst = {}
+    for g0 in range(0, len(valid), 8):
+        part = slice(g0, g0 + 8)
+        sub = model.forward_batch(ids[part], valid[part], pos[part], mask[part], qtype[part])
+        for f in fields:
+            name = "act_features" if f == "features" else f
+            _compare(name, getattr(sub, f), getattr(out, f)[part], worst)
+    print({k: f"{a:.1e}/{r:.1e}" for k, (a, r) in worst.items()}, flush=True)
