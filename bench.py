@@ -3,6 +3,7 @@
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10] [--workload NAME] [--no-encoder]
     python bench.py --refbench [--refbench-out PATH]
+    python bench.py --predict [--predict-tokens 512,2048,4096] [--predict-repeats 20]
 
 A step is one launch of the fused fp32 attention kernel over one whole batch
 whose Q, K, V (seeded N(0, 1)) are already resident in HBM; successive steps
@@ -45,6 +46,11 @@ With the default workload the line also carries:
 row per kernel x mask x seq x threads with mean_ms, stddev_ms, samples and
 stages, for this GPU beside the Tiled restatement (1 thread and all threads) and
 Naive (1 thread) on 16 heads x L in {2048, 4096, 8192} x {Block3, Window64}.
+
+--predict prints the predict-latency document that `raya bench` is specified to write
+(specs/008-bench-harness/spec.md:19-31): one sequence of each token count through the
+12-layer decision model, p50/p90 of the end-to-end call, the per-component split, the model's
+load time and the peak RSS.
 """
 from __future__ import annotations
 
@@ -752,6 +758,80 @@ def refbench(out_path: str | None, samples: int, naive_samples: int, cpu: bool) 
     return doc
 
 
+def predict_bench(tokens: list[int], repeats: int, warmup: int, cap_s: float) -> dict:
+    """End-to-end predict latency of the decision model for one sequence of each length,
+    as `raya bench` is specified (specs/008-bench-harness/spec.md:19-31, FR-001/FR-002): the
+    bench's synthetic 12-layer checkpoint loaded once (load time reported apart), a fixed
+    synthetic token input with one question (markers at positions 1 and 2, qtype 0), p50 and
+    p90 over `repeats` calls after `warmup`, each call from host arrays to host outputs, the
+    per-component split (embedding, each encoder layer, final norm, head) from the forward's
+    own stage spans, peak RSS and whether the time cap cut a length short.  The reference's
+    output-parity gate (FR-003) compares with saved Laya outputs, which this repository does
+    not hold; the forward's parity is held by the test suite instead."""
+    import resource
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from raya_amd import checkpoint, model as M, synth
+
+    tmp = tempfile.mkdtemp(prefix="raya_ckpt_")
+    rows = []
+    try:
+        log("predict: writing the synthetic checkpoint")
+        checkpoint.write_synthetic(tmp, seed=ENCODER_WEIGHT_SEED)
+        t0 = time.perf_counter()
+        m = M.Model.load(tmp)
+        load_ms = (time.perf_counter() - t0) * 1e3
+        info = m.info
+        for n in tokens:
+            if n > info["max_position_embeddings"]:
+                rows.append({"tokens": n, "skipped": f"past max_position_embeddings "
+                                                     f"{info['max_position_embeddings']}"})
+                continue
+            ids = (synth.uniform(synth.workload_seed(4, 20), n) * (info["vocab_size"] - 1)).astype(np.uint32)
+            ids = ids.reshape(1, n)
+            ids[0, 0] = 101  # the [CLS] id the encoder workload starts with
+            valid = np.array([n], np.uint64)
+            pos = np.array([[1, 2]], np.uint64)
+            mask = np.ones((1, 2), np.uint8)
+            qtype = np.zeros(1, np.uint64)
+            log(f"predict: {n} tokens, warmup {warmup}, {repeats} calls")
+            for _ in range(warmup):
+                m.forward_batch(ids, valid, pos, mask, qtype)
+            lat, capped, t_start = [], False, time.perf_counter()
+            for _ in range(repeats):
+                t1 = time.perf_counter()
+                out = m.forward_batch(ids, valid, pos, mask, qtype)
+                lat.append((time.perf_counter() - t1) * 1e3)
+                if time.perf_counter() - t_start > cap_s:
+                    capped = True
+                    break
+            m.set_profiling(1)
+            try:
+                m.forward_batch(ids, valid, pos, mask, qtype)
+                parts = m.stage_times()
+            finally:
+                m.set_profiling(0)
+            lat.sort()
+            rows.append({
+                "tokens": n, "calls": len(lat), "p50_ms": lat[len(lat) // 2],
+                "p90_ms": lat[min(len(lat) - 1, (9 * len(lat)) // 10)], "mean_ms": statistics.mean(lat),
+                "time_cap_hit": capped, "components_ms": {name: ms for name, ms in parts},
+                "probabilities": [float(x) for x in out.probabilities[0]],
+            })
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    return {
+        "bench": "predict latency (raya bench, specs/008-bench-harness)", "model": "12-layer ModernBERT-base "
+        "width synthetic checkpoint (N(0, 0.02) weights, vocab 30,522, max positions 4,096)",
+        "model_load_ms": load_ms, "warmup": warmup, "repeats": repeats, "time_cap_s": cap_s,
+        "peak_rss_mb": resource.getrusage(resource.RUSAGE_SELF).ru_maxrss / 1024.0,
+        "attention_kernel": "hip-gfx950", "results": rows,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -771,6 +851,12 @@ def main() -> int:
     ap.add_argument("--refbench-out", default=None)
     ap.add_argument("--refbench-samples", type=int, default=10)
     ap.add_argument("--refbench-naive-samples", type=int, default=3)
+    ap.add_argument("--predict", action="store_true",
+                    help="print the predict-latency document (raya bench) instead of the bench line")
+    ap.add_argument("--predict-tokens", default="512,2048,4096")
+    ap.add_argument("--predict-repeats", type=int, default=20)
+    ap.add_argument("--predict-warmup", type=int, default=3)
+    ap.add_argument("--predict-cap-s", type=float, default=60.0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
@@ -785,6 +871,12 @@ def main() -> int:
         print(json.dumps({"refbench_rows": len(doc["results"]), "label": doc["label"],
                           "gpu_rows": [{k: r[k] for k in ("mask", "seq", "mean_ms", "stddev_ms")}
                                        for r in doc["results"] if r["kernel"] == "hip"]}), flush=True)
+        return 0
+
+    if args.predict:
+        doc = predict_bench([int(x) for x in args.predict_tokens.split(",")], args.predict_repeats,
+                            args.predict_warmup, args.predict_cap_s)
+        print(json.dumps(doc), flush=True)
         return 0
 
     if args.gemm_only:
