@@ -402,8 +402,13 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
     constexpr int OUT_BN = GEGLU ? BN / 2 : BN;
     const int tiles_n = (g.n + OUT_BN - 1) / OUT_BN;
     const int tiles_m = (g.m + BM - 1) / BM;
+    // Split-K: workgroups tile * S .. tile * S + S - 1 share one output tile (the
+    // reducing launch: one workgroup per tile).
+    const int S = g.splits > 1 ? g.splits : 1;
+    const int tile = g.reduce ? (int)blockIdx.x : (int)blockIdx.x / S;
+    const int split = (int)blockIdx.x - tile * S;
     int tm, tn;
-    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+    tile_of(tile, tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * OUT_BN;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -448,8 +453,10 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
         bsrc[j] = g.b + (int64_t)brow * g.ldb + 4 * c;
     }
     const uint32_t ring_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr_t *)ring);
+    const int nk = g.k / RBK / S;  // this workgroup's slabs: split * nk .. split * nk + nk - 1
+    const int slab0 = split * nk;
     const auto issue = [&](int slab, int stage) {
-        const int k0 = slab * RBK;
+        const int k0 = (slab0 + slab) * RBK;
         const uint32_t sa = ring_base + (uint32_t)(stage * 2 * kTileFloats * 4);
 #pragma unroll
         for (int j = 0; j < 2; ++j) dma16(asrc[j] + k0, sa + (2 * wave + j) * 1024);
@@ -465,45 +472,87 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    const int nk = g.k / RBK;
-    issue(0, 0);
-    if (nk > 1) issue(1, 1);
-    int stage = 0;
-    for (int kt = 0; kt < nk; ++kt) {
-        // Each wave issued 4 DMAs per slab: with slab kt + 1 in flight, vmcnt(4)
-        // means slab kt has landed; the barrier makes that hold for every wave and
-        // retires the reads of the stage slab kt + 2 goes into.
-        if (kt + 1 < nk)
-            asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-        else
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        barrier_only();
-        if (kt + 2 < nk) issue(kt + 2, stage == 0 ? 2 : stage - 1);
-        // The slab's operand reads and MFMAs run at raised wave priority, so a
-        // wave that has passed its barrier keeps the matrix core busy while the
-        // other workgroups' waves wait at theirs: the three workgroups of a CU
-        // drift out of step instead of stalling together (+2-5% on the encoder
-        // shapes against equal priority).
-        __builtin_amdgcn_s_setprio(1);
-        const float *As = ring + stage * 2 * kTileFloats, *Bs = As + kTileFloats;
+    constexpr int kTile4 = BM * BN / 4, kWave4 = kTile4 / 4;
+    if (g.reduce) {
+        // The partials of this tile, summed in split order, a whole partial's 16 loads per
+        // lane in flight at a time.
+        const float4 *all = (const float4 *)g.partials + (int64_t)tile * S * kTile4 + wave * kWave4;
+        float4 t[16];
 #pragma unroll
-        for (int kc = 0; kc < RBK / 4; kc += 2) {
-            float4 av[2], bv[2];
+        for (int q = 0; q < 16; ++q) t[q] = all[q * 64 + lane];
+        for (int s2 = 1; s2 < S; ++s2) {
+            float4 u[16];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int ra = wm + 32 * i + li, rb = wn + 32 * i + li;
-                av[i] = *(const float4 *)&As[ra * RBK + 4 * ((kc + h) ^ rswz(ra))];
-                bv[i] = *(const float4 *)&Bs[rb * RBK + 4 * ((kc + h) ^ rswz(rb))];
+            for (int q = 0; q < 16; ++q) u[q] = all[(int64_t)s2 * kTile4 + q * 64 + lane];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                t[q].x += u[q].x;
+                t[q].y += u[q].y;
+                t[q].z += u[q].z;
+                t[q].w += u[q].w;
             }
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(av[i][s], bv[j][s], acc[i][j]);
         }
-        __builtin_amdgcn_s_setprio(0);
-        stage = stage == RSTAGES - 1 ? 0 : stage + 1;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            floatx16 &x = acc[q >> 3][(q >> 2) & 1];
+            const int r = 4 * (q & 3);
+            x[r] = t[q].x;
+            x[r + 1] = t[q].y;
+            x[r + 2] = t[q].z;
+            x[r + 3] = t[q].w;
+        }
+    } else {
+        issue(0, 0);
+        if (nk > 1) issue(1, 1);
+        int stage = 0;
+        for (int kt = 0; kt < nk; ++kt) {
+            // Each wave issued 4 DMAs per slab: with slab kt + 1 in flight, vmcnt(4)
+            // means slab kt has landed; the barrier makes that hold for every wave and
+            // retires the reads of the stage slab kt + 2 goes into.
+            if (kt + 1 < nk)
+                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            barrier_only();
+            if (kt + 2 < nk) issue(kt + 2, stage == 0 ? 2 : stage - 1);
+            // The slab's operand reads and MFMAs run at raised wave priority, so a
+            // wave that has passed its barrier keeps the matrix core busy while the
+            // other workgroups' waves wait at theirs: the three workgroups of a CU
+            // drift out of step instead of stalling together (+2-5% on the encoder
+            // shapes against equal priority).
+            __builtin_amdgcn_s_setprio(1);
+            const float *As = ring + stage * 2 * kTileFloats, *Bs = As + kTileFloats;
+#pragma unroll
+            for (int kc = 0; kc < RBK / 4; kc += 2) {
+                float4 av[2], bv[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int ra = wm + 32 * i + li, rb = wn + 32 * i + li;
+                    av[i] = *(const float4 *)&As[ra * RBK + 4 * ((kc + h) ^ rswz(ra))];
+                    bv[i] = *(const float4 *)&Bs[rb * RBK + 4 * ((kc + h) ^ rswz(rb))];
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(av[i][s], bv[j][s], acc[i][j]);
+            }
+            __builtin_amdgcn_s_setprio(0);
+            stage = stage == RSTAGES - 1 ? 0 : stage + 1;
+        }
+        if (S > 1) {
+            // The partial tile goes out in the accumulator layout (each wave's 64 x 64 quadrant
+            // as 16 lane-contiguous float4 rows); the reducing launch reads it back.
+            float4 *mine = (float4 *)g.partials + ((int64_t)tile * S + split) * kTile4 + wave * kWave4;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const floatx16 &x = acc[q >> 3][(q >> 2) & 1];
+                const int r = 4 * (q & 3);
+                mine[q * 64 + lane] = make_float4(x[r], x[r + 1], x[r + 2], x[r + 3]);
+            }
+            return;
+        }
     }
     const bool vec_out = (g.ldo & 3) == 0 && ((uintptr_t)g.out & 15) == 0 &&
                          (!g.residual || ((g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15) == 0));
@@ -528,8 +577,12 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
     if (tiles > 0x7fffffff / kThreads) return hipErrorInvalidValue;
     const bool vec = (g.lda % 4 == 0) && (g.ldb % 4 == 0) && (((uintptr_t)g.a & 15) == 0) &&
                      (((uintptr_t)g.b & 15) == 0) && (g.k % 4 == 0);
-    const dim3 grid((unsigned)tiles), block(kThreads);
     const bool ring_ok = vec && g.k % RBK == 0 && g.k > 0;
+    const int splits = g.splits > 1 ? g.splits : 1;
+    if (g.reduce || (splits > 1 && (!ring_ok || !g.partials || tiles > kGemmSplitMaxTiles || splits > 16 ||
+                                    (g.k / RBK) % splits != 0)))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(tiles * splits)), block(kThreads);
     if (g.in_stats || g.out_stats) {
         // Only the ring kernel's staged epilogue carries them (see GemmLaunch).
         const bool vec_out = (g.ldo & 3) == 0 && ((uintptr_t)g.out & 15) == 0 &&
@@ -545,22 +598,31 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
     }
     if (ring_ok) {
         constexpr bool NONE = ACT == RAYA_EPI_NONE;
-        if (g.in_stats) {  // folded LayerNorm: QKV (with or without RoPE) and GeGLU
-            if (g.rope_cos)
-                hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE, true>), grid, block, 0, stream, g);
-            else
-                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, true>), grid, block, 0, stream, g);
-        } else if (g.out_stats) {  // the residual GEMMs
-            if constexpr (NONE)
-                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, false, true>), grid, block, 0, stream, g);
-            else
-                return hipErrorInvalidValue;
-        } else if (g.rope_cos) {
-            hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE>), grid, block, 0, stream, g);
-        } else {
-            hipLaunchKernelGGL((gemm_ring_kernel<ACT, false>), grid, block, 0, stream, g);
-        }
-        return hipGetLastError();
+        const auto ring = [&](const GemmLaunch &gg, dim3 gr) -> hipError_t {
+            if (gg.in_stats) {  // folded LayerNorm: QKV (with or without RoPE) and GeGLU
+                if (gg.rope_cos)
+                    hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE, true>), gr, block, 0, stream, gg);
+                else
+                    hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, true>), gr, block, 0, stream, gg);
+            } else if (gg.out_stats) {  // the residual GEMMs
+                if constexpr (NONE)
+                    hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, false, true>), gr, block, 0, stream, gg);
+                else
+                    return hipErrorInvalidValue;
+            } else if (gg.rope_cos) {
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE>), gr, block, 0, stream, gg);
+            } else {
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false>), gr, block, 0, stream, gg);
+            }
+            return hipGetLastError();
+        };
+        hipError_t e = ring(g, grid);
+        if (e != hipSuccess || splits == 1) return e;
+        // Split-K: the partial tiles are complete when the first launch ends; one workgroup
+        // per tile sums them and runs the epilogue.
+        GemmLaunch r = g;
+        r.reduce = 1;
+        return ring(r, dim3((unsigned)tiles));
     }
     if constexpr (ACT == RAYA_EPI_NONE) {
         if (g.rope_cos) {
@@ -599,6 +661,30 @@ hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream) {
     case RAYA_EPI_GEGLU: return launch_act<RAYA_EPI_GEGLU>(g, stream);
     default: return hipErrorInvalidValue;
     }
+}
+
+// MI355X: 256 compute units, 3 ring-kernel workgroups each.  A launch of few tiles (few
+// rows: one short sequence) runs each tile's K loop on one workgroup, whose slabs then wait
+// on HBM one after another; splitting K fills the units' slots and shortens those chains,
+// keeping at least 4 slabs (64 k) per workgroup.
+constexpr int kWorkgroupSlots = 3 * 256;
+constexpr int kMaxSplits = 8;
+
+int gemm_splits(int m, int n, int k, int act) {
+    const int out_bn = act == RAYA_EPI_GEGLU ? BN / 2 : BN;
+    const int64_t tiles = (int64_t)((m + BM - 1) / BM) * ((n + out_bn - 1) / out_bn);
+    if (m <= 0 || n <= 0 || k <= 0 || k % RBK != 0 || tiles > kGemmSplitMaxTiles) return 1;
+    const int nk = k / RBK;
+    int s = (int)std::min<int64_t>(kMaxSplits, kWorkgroupSlots / tiles);
+    while (s > 1 && (nk % s != 0 || nk / s < 4)) --s;
+    return s > 1 ? s : 1;
+}
+
+size_t gemm_split_floats(int m, int n, int act, int splits) {
+    if (splits <= 1) return 0;
+    const int out_bn = act == RAYA_EPI_GEGLU ? BN / 2 : BN;
+    const size_t tiles = (size_t)((m + BM - 1) / BM) * ((n + out_bn - 1) / out_bn);
+    return tiles * (size_t)splits * BM * BN;
 }
 
 hipError_t launch_fill_zero(float *out, int64_t ldo, int m, int n, hipStream_t stream) {

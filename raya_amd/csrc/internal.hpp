@@ -69,7 +69,22 @@ struct GemmLaunch {
     // (mean, M2) of each output row over each 64-column chunk, after the
     // residual add ([m][n / 64]); n a multiple of 64.  Null: off.
     float2 *out_stats;
+    // Split-K (the ring kernel only), for launches whose output tiles alone leave
+    // compute units idle: each tile's K loop is divided among `splits` workgroups,
+    // which store their partial tiles to `partials` ([tiles][splits][128 x 128]);
+    // a second launch of the same kernel (reduce = 1, set by launch_gemm) sums each
+    // tile's partials in split order and runs the epilogue.  splits <= 1: off.
+    float *partials;
+    int32_t splits;
+    int32_t reduce;
 };
+
+// Split-K for the ring kernel: the split count gemm_splits chooses for an
+// m x n output (GeGLU: n output columns from 2n weight rows) of depth k (1: no
+// split; never past kGemmSplitMaxTiles output tiles), and the partials' floats.
+constexpr int kGemmSplitMaxTiles = 256;
+int gemm_splits(int m, int n, int k, int act);
+size_t gemm_split_floats(int m, int n, int act, int splits);
 
 // Head dim of the fused RoPE epilogue (other head dims use launch_rope).
 constexpr int kRopeHeadDim = 64;

@@ -917,6 +917,18 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
 
     const uint64_t inter = c.inter, big = std::max(inter, c.head_ffn), nact = c.n_act;
     const uint64_t BK = B * K;
+    // Split-K partials for the encoder GEMMs when the tokens are too few for their tiles to
+    // fill the compute units (a single short sequence); other GEMMs split only if they fit.
+    size_t split_cap = 0;
+    {
+        const uint64_t shapes[4][3] = {{3 * d, d, RAYA_EPI_NONE}, {d, d, RAYA_EPI_NONE}, {inter, d, RAYA_EPI_GEGLU},
+                                       {d, inter, RAYA_EPI_NONE}};
+        for (const auto &sh : shapes) {
+            const int act = (int)sh[2];
+            split_cap = std::max(split_cap, gemm_split_floats((int)T, (int)sh[0], act,
+                                                              gemm_splits((int)T, (int)sh[0], (int)sh[1], act)));
+        }
+    }
     size_t need = 0;
     {
         Carve probe{nullptr};
@@ -936,6 +948,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         probe.take<float>(B * nact);     // act logits
         probe.take<float>(T * (d / 64) * 2);  // LayerNorm chunk statistics of h
         probe.take<float>(T * 2);             // and each row's (mean, rstd)
+        probe.take<float>(split_cap);         // split-K partial tiles
         need = probe.off;
     }
     if ((rc = dm.work.reserve(need))) return rc;
@@ -953,6 +966,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     float *d_act = cv.take<float>(B * nact);
     float2 *hstats = (float2 *)cv.take<float>(T * (d / 64) * 2);
     float2 *hrow = (float2 *)cv.take<float>(T * 2);
+    float *partials = cv.take<float>(split_cap);
     const int32_t *d_ids = d_ints + o_ids, *d_pos = d_ints + o_pos, *d_rowseq = d_ints + o_rs;
     const int32_t *d_start = d_ints + o_start, *d_valid = d_ints + o_valid, *d_qtype = d_ints + o_q;
     const int32_t *d_mrow = d_ints + o_mrow;
@@ -1030,6 +1044,17 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
 #define SPAN_END(slot) RECORD(span_end(slot))
 
     auto P = [&](const std::string &name) { return param(m, dm, name); };
+    // Split-K for a ring-kernel launch whose tiles leave compute units idle, when its
+    // partials fit the carved space (the launches run in order on one stream and share it).
+    auto set_split = [&](GemmLaunch &g) {
+        const bool ring = g.k % 16 == 0 && g.lda % 4 == 0 && g.ldb % 4 == 0 && ((uintptr_t)g.a & 15) == 0 &&
+                          ((uintptr_t)g.b & 15) == 0;
+        const int sp = ring ? gemm_splits(g.m, g.n, g.k, g.act) : 1;
+        if (sp > 1 && gemm_split_floats(g.m, g.n, g.act, sp) <= split_cap) {
+            g.splits = sp;
+            g.partials = partials;
+        }
+    };
     auto gemm = [&](float *o, int64_t ldo, const float *a, int64_t lda, const float *wt, uint64_t rows, uint64_t n,
                     uint64_t k, int act, const float *bias, const float *res) -> int {
         GemmLaunch g{};
@@ -1047,6 +1072,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         g.bias = bias;
         g.residual = res;
         g.ldr = ldo;
+        set_split(g);
         TRY_HIP(launch_gemm(g, stream), "gemm");
         return RAYA_OK;
     };
@@ -1068,6 +1094,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         g.residual = h;
         g.ldr = (int64_t)d;
         g.out_stats = stats ? hstats : nullptr;
+        set_split(g);
         TRY_HIP(launch_gemm(g, stream), "residual gemm");
         if (stats)
             TRY_HIP(launch_ln_stats(hstats, (int)T, (int)(d / 64), (float)c.norm_eps, hrow, stream), "ln stats");
@@ -1171,6 +1198,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
                 g.positions = d_pos;
                 g.rope_cols = (int32_t)(2 * d);
             }
+            set_split(g);
             TRY_HIP(launch_gemm(g, stream), "qkv gemm");
             if (hd != (uint64_t)kRopeHeadDim)
                 TRY_HIP(launch_rope(qkv, (int64_t)(3 * d), d_pos, cos_t, sin_t, (int)T, (int)d, (int)hd, stream),
@@ -1205,6 +1233,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
             g.act = RAYA_EPI_GEGLU;
             g.in_stats = hrow;
             g.colsum = folded + dm.folded.wi_sum[i];
+            set_split(g);
             TRY_HIP(launch_gemm(g, stream), "mlp in gemm");
         } else {
             RECORD(gemm(gated, inter, nb, d, P(p + ".mlp.Wi.weight"), T, inter, d, RAYA_EPI_GEGLU, nullptr, nullptr));
