@@ -151,22 +151,24 @@ __global__ void gather_rows_kernel(const float *h, int64_t ldh, const int32_t *r
 // (head.rs:70-92) for one sequence per thread, in the reference's sequential
 // f32 order: invalid markers' logits become -1e4, softmax_in_place
 // (ops.rs:77-87), [top1, top1 - top2, entropy / ln k, k / 255] with
-// k = max(valid markers, 2), pooled = row 0, act_in = [pooled, features].
+// k = max(valid markers, 2), pooled = row 0, act_in = [pooled, features] in rows of
+// ld_act floats whose columns past d + 4 are zero (the act head's padded depth).
 __global__ void head_finish_kernel(const float *raw_logits, const uint8_t *mask, int batch,
                                    int markers, const float *h, int64_t ldh,
                                    const int32_t *seq_start, int d, float *logits, float *probs,
-                                   float *features, float *pooled, float *act_in) {
+                                   float *features, float *pooled, float *act_in, int ld_act) {
     // One workgroup per sequence: every thread copies part of the CLS row; thread 0
     // runs the marker softmax and the features in the reference's sequential order.
     const int b = blockIdx.x;
     if (b >= batch) return;
     const float *row0 = h + (int64_t)seq_start[b] * ldh;
-    float *ai = act_in + (int64_t)b * (d + 4);
+    float *ai = act_in + (int64_t)b * ld_act;
     for (int c = threadIdx.x; c < d; c += blockDim.x) {
         const float x = row0[c];
         pooled[(int64_t)b * d + c] = x;
         ai[c] = x;
     }
+    for (int c = d + 4 + threadIdx.x; c < ld_act; c += blockDim.x) ai[c] = 0.0f;
     if (threadIdx.x != 0) return;
     const float *raw = raw_logits + (int64_t)b * markers;
     const uint8_t *mk = mask + (int64_t)b * markers;
@@ -290,11 +292,12 @@ hipError_t launch_gather_rows(const float *h, int64_t ldh, const int32_t *rows, 
 hipError_t launch_head_finish(const float *raw_logits, const uint8_t *mask, int batch, int markers,
                               const float *h, int64_t ldh, const int32_t *seq_start, int d,
                               float *logits, float *probs, float *features, float *pooled,
-                              float *act_in, hipStream_t stream) {
+                              float *act_in, int ld_act, hipStream_t stream) {
     if (batch == 0) return hipSuccess;
+    if (ld_act < d + 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(head_finish_kernel, dim3((unsigned)batch), dim3(256), 0, stream,
                        raw_logits, mask, batch, markers, h, ldh, seq_start, d, logits, probs,
-                       features, pooled, act_in);
+                       features, pooled, act_in, ld_act);
     return hipGetLastError();
 }
 

@@ -119,7 +119,7 @@ hipError_t launch_gather_rows(const float *h, int64_t ldh, const int32_t *rows, 
 hipError_t launch_head_finish(const float *raw_logits, const uint8_t *mask, int batch, int markers,
                               const float *h, int64_t ldh, const int32_t *seq_start, int d,
                               float *logits, float *probs, float *features, float *pooled,
-                              float *act_in, hipStream_t stream);
+                              float *act_in, int ld_act, hipStream_t stream);
 
 // Thread-local error state of the C ABI (capi.cpp).
 int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));

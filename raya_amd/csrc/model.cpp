@@ -590,6 +590,7 @@ struct DeviceModel {
     DeviceBuf rope;  // global cos, global sin, local cos, local sin: [rope_len][head_dim / 2] each
     int rope_len = 0;
     DeviceBuf work;
+    DeviceBuf act_w;  // act_head.0.weight [256][d + 4] with its rows padded by zeros to ld_act
     FoldedNorms folded;
 };
 
@@ -627,6 +628,21 @@ int ensure_device(Model &m, DeviceModel **out) {
         slot = std::move(dm);
     }
     *out = slot.get();
+    return RAYA_OK;
+}
+
+int ensure_act_weight(const Model &m, DeviceModel &dm, uint64_t ld_act) {
+    if (dm.act_w.ptr) return RAYA_OK;
+    auto it = m.w.index.find("act_head.0.weight");
+    if (it == m.w.index.end()) return fail(RAYA_ERR_WEIGHTS, "missing act_head.0.weight");
+    const uint64_t k = m.cfg.hidden + 4, rows = 256;
+    const float *src = m.w.host.data() + m.w.entries[it->second].offset;
+    std::vector<float> host(rows * ld_act, 0.0f);
+    for (uint64_t r = 0; r < rows; ++r) memcpy(host.data() + r * ld_act, src + r * k, k * sizeof(float));
+    int rc = dm.act_w.reserve(host.size() * sizeof(float));
+    if (rc) return rc;
+    const hipError_t e = hipMemcpy(dm.act_w.ptr, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail_device(e, "upload the padded act head weight");
     return RAYA_OK;
 }
 
@@ -917,6 +933,10 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
 
     const uint64_t inter = c.inter, big = std::max(inter, c.head_ffn), nact = c.n_act;
     const uint64_t BK = B * K;
+    // The act head's first Linear has depth d + 4; its input rows and weight are padded with
+    // zeros to a multiple of 16 so that it runs on the ring kernel (and splits K).
+    const uint64_t ld_act = (d + 4 + 15) / 16 * 16;
+    if ((rc = ensure_act_weight(m, dm, ld_act))) return rc;
     // Split-K partials for the encoder GEMMs when the tokens are too few for their tiles to
     // fill the compute units (a single short sequence); other GEMMs split only if they fit.
     size_t split_cap = 0;
@@ -943,7 +963,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         probe.take<float>(BK * 3);       // raw logits, logits, probabilities
         probe.take<float>(B * 4);        // features
         probe.take<float>(B * d);        // pooled
-        probe.take<float>(B * (d + 4));  // act input
+        probe.take<float>(B * ld_act);   // act input, rows padded to the act head's depth
         probe.take<float>(B * 256);      // act hidden
         probe.take<float>(B * nact);     // act logits
         probe.take<float>(T * (d / 64) * 2);  // LayerNorm chunk statistics of h
@@ -962,7 +982,7 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     float *raw = cv.take<float>(BK * 3);
     float *d_logits = raw + BK, *d_probs = raw + 2 * BK;
     float *d_feat = cv.take<float>(B * 4), *d_pooled = cv.take<float>(B * d);
-    float *act_in = cv.take<float>(B * (d + 4)), *act_hid = cv.take<float>(B * 256);
+    float *act_in = cv.take<float>(B * ld_act), *act_hid = cv.take<float>(B * 256);
     float *d_act = cv.take<float>(B * nact);
     float2 *hstats = (float2 *)cv.take<float>(T * (d / 64) * 2);
     float2 *hrow = (float2 *)cv.take<float>(T * 2);
@@ -1300,13 +1320,13 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     RECORD(gemm(s_hid, d, s_norm, d, P("scorer.1.weight"), BK, d, d, RAYA_EPI_GELU, P("scorer.1.bias"), nullptr));
     RECORD(gemm(raw, 1, s_hid, d, P("scorer.3.weight"), BK, 1, d, RAYA_EPI_NONE, P("scorer.3.bias"), nullptr));
     TRY_HIP(launch_head_finish(raw, d_mask, (int)B, (int)K, h, (int64_t)d, d_start, (int)d, d_logits, d_probs, d_feat,
-                               d_pooled, act_in, stream),
+                               d_pooled, act_in, (int)ld_act, stream),
             "head finish");
     RECORD(record_dense("logits", d_logits, {B, K}));
     RECORD(record_dense("probabilities", d_probs, {B, K}));
     RECORD(record_dense("act_features", d_feat, {B, 4}));
     RECORD(record_dense("pooled", d_pooled, {B, d}));
-    RECORD(gemm(act_hid, 256, act_in, d + 4, P("act_head.0.weight"), B, 256, d + 4, RAYA_EPI_GELU,
+    RECORD(gemm(act_hid, 256, act_in, ld_act, (const float *)dm.act_w.ptr, B, 256, ld_act, RAYA_EPI_GELU,
                 P("act_head.0.bias"), nullptr));
     RECORD(gemm(d_act, nact, act_hid, 256, P("act_head.2.weight"), B, nact, 256, RAYA_EPI_NONE, P("act_head.2.bias"),
                 nullptr));
