@@ -31,7 +31,8 @@ With the default workload the line also carries:
 * "encoder": sequences/sec of the full 12-layer ModernBERT-base decision-model
   forward (B=64, L=512, valid lengths uniform in [128, 512], random N(0, 0.02)
   weights from a safetensors checkpoint) and the oracle's CPU forward on the
-  first sequences beside it;
+  first sequences beside it; "predict_latency" in it: p50/p90 of single-sequence
+  predicts of 512, 2,048 and 4,096 tokens (end to end, host arrays in and out);
 * "encoder_layer": one block-local layer of that model on B=16 x L=1024 valid
   tokens (BlockDiag(64) on the local layers), from the forward's own per-layer
   event spans;
@@ -436,6 +437,9 @@ def bench_encoder(steps: int, warmup: int, cpu_seconds: float, cpu: bool, layer:
         }
         if layer:
             res["layer"] = bench_layer(m, steps, warmup)
+            # one sequence per call, as raya predict runs: end-to-end latency
+            res["predict_latency"] = [{k: r[k] for k in ("tokens", "p50_ms", "p90_ms", "calls")}
+                                      for r in predict_rows(m, [512, 2048, 4096], 20, 3, 30.0)]
         if cpu:
             log("encoder: cpu baseline")
             res["cpu_baseline"] = encoder_cpu_baseline(tmp, ids, valid, pos, mask, qtype, out,
@@ -758,6 +762,54 @@ def refbench(out_path: str | None, samples: int, naive_samples: int, cpu: bool) 
     return doc
 
 
+def predict_rows(m, tokens: list[int], repeats: int, warmup: int, cap_s: float) -> list[dict]:
+    """p50/p90 of end-to-end predicts of one sequence of each length on a loaded model (see
+    predict_bench), with the forward's per-component split."""
+    import numpy as np
+
+    from raya_amd import synth
+
+    info = m.info
+    rows = []
+    for n in tokens:
+        if n > info["max_position_embeddings"]:
+            rows.append({"tokens": n, "skipped": f"past max_position_embeddings "
+                                                 f"{info['max_position_embeddings']}"})
+            continue
+        ids = (synth.uniform(synth.workload_seed(4, 20), n) * (info["vocab_size"] - 1)).astype(np.uint32)
+        ids = ids.reshape(1, n)
+        ids[0, 0] = 101  # the [CLS] id the encoder workload starts with
+        valid = np.array([n], np.uint64)
+        pos = np.array([[1, 2]], np.uint64)
+        mask = np.ones((1, 2), np.uint8)
+        qtype = np.zeros(1, np.uint64)
+        log(f"predict: {n} tokens, warmup {warmup}, {repeats} calls")
+        for _ in range(warmup):
+            m.forward_batch(ids, valid, pos, mask, qtype)
+        lat, capped, t_start = [], False, time.perf_counter()
+        for _ in range(repeats):
+            t1 = time.perf_counter()
+            out = m.forward_batch(ids, valid, pos, mask, qtype)
+            lat.append((time.perf_counter() - t1) * 1e3)
+            if time.perf_counter() - t_start > cap_s:
+                capped = True
+                break
+        m.set_profiling(1)
+        try:
+            m.forward_batch(ids, valid, pos, mask, qtype)
+            parts = m.stage_times()
+        finally:
+            m.set_profiling(0)
+        lat.sort()
+        rows.append({
+            "tokens": n, "calls": len(lat), "p50_ms": lat[len(lat) // 2],
+            "p90_ms": lat[min(len(lat) - 1, (9 * len(lat)) // 10)], "mean_ms": statistics.mean(lat),
+            "time_cap_hit": capped, "components_ms": {name: ms for name, ms in parts},
+            "probabilities": [float(x) for x in out.probabilities[0]],
+        })
+    return rows
+
+
 def predict_bench(tokens: list[int], repeats: int, warmup: int, cap_s: float) -> dict:
     """End-to-end predict latency of the decision model for one sequence of each length,
     as `raya bench` is specified (specs/008-bench-harness/spec.md:19-31, FR-001/FR-002): the
@@ -772,9 +824,7 @@ def predict_bench(tokens: list[int], repeats: int, warmup: int, cap_s: float) ->
     import shutil
     import tempfile
 
-    import numpy as np
-
-    from raya_amd import checkpoint, model as M, synth
+    from raya_amd import checkpoint, model as M
 
     tmp = tempfile.mkdtemp(prefix="raya_ckpt_")
     rows = []
@@ -784,43 +834,7 @@ def predict_bench(tokens: list[int], repeats: int, warmup: int, cap_s: float) ->
         t0 = time.perf_counter()
         m = M.Model.load(tmp)
         load_ms = (time.perf_counter() - t0) * 1e3
-        info = m.info
-        for n in tokens:
-            if n > info["max_position_embeddings"]:
-                rows.append({"tokens": n, "skipped": f"past max_position_embeddings "
-                                                     f"{info['max_position_embeddings']}"})
-                continue
-            ids = (synth.uniform(synth.workload_seed(4, 20), n) * (info["vocab_size"] - 1)).astype(np.uint32)
-            ids = ids.reshape(1, n)
-            ids[0, 0] = 101  # the [CLS] id the encoder workload starts with
-            valid = np.array([n], np.uint64)
-            pos = np.array([[1, 2]], np.uint64)
-            mask = np.ones((1, 2), np.uint8)
-            qtype = np.zeros(1, np.uint64)
-            log(f"predict: {n} tokens, warmup {warmup}, {repeats} calls")
-            for _ in range(warmup):
-                m.forward_batch(ids, valid, pos, mask, qtype)
-            lat, capped, t_start = [], False, time.perf_counter()
-            for _ in range(repeats):
-                t1 = time.perf_counter()
-                out = m.forward_batch(ids, valid, pos, mask, qtype)
-                lat.append((time.perf_counter() - t1) * 1e3)
-                if time.perf_counter() - t_start > cap_s:
-                    capped = True
-                    break
-            m.set_profiling(1)
-            try:
-                m.forward_batch(ids, valid, pos, mask, qtype)
-                parts = m.stage_times()
-            finally:
-                m.set_profiling(0)
-            lat.sort()
-            rows.append({
-                "tokens": n, "calls": len(lat), "p50_ms": lat[len(lat) // 2],
-                "p90_ms": lat[min(len(lat) - 1, (9 * len(lat)) // 10)], "mean_ms": statistics.mean(lat),
-                "time_cap_hit": capped, "components_ms": {name: ms for name, ms in parts},
-                "probabilities": [float(x) for x in out.probabilities[0]],
-            })
+        rows = predict_rows(m, tokens, repeats, warmup, cap_s)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
     return {
