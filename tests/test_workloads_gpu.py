@@ -152,3 +152,27 @@ def test_twelve_layer_encoder_batch_order_and_size(tmp_path):
             name = "act_features" if f == "features" else f
             _compare(name, getattr(sub, f), getattr(out, f)[part], worst)
     print({k: f"{a:.1e}/{r:.1e}" for k, (a, r) in worst.items()}, flush=True)
+
+
+@pytest.mark.timeout(600)
+def test_split_k_forward_matches_the_unsplit_batch(tmp_path):
+    """One sequence alone (few rows: every encoder GEMM and the act head split K into partial
+    tiles and a reducing launch) against the same sequence inside the bench's batch of 64
+    (thousands of rows: no GEMM splits), every output at the fp32 bar; and the split forward
+    run twice gives the same bits (the partials are summed in a fixed order)."""
+    spec = W.ENCODER
+    ckpt = str(tmp_path / "enc")
+    checkpoint.write_synthetic(ckpt, seed=W.ENCODER_WEIGHT_SEED)
+    model = M.Model.load(ckpt)
+    ids, valid, pos, mask, qtype = W.encoder_inputs(spec)
+    batch = model.forward_batch(ids, valid, pos, mask, qtype)
+    fields = ("logits", "probabilities", "act_logits", "features", "pooled")
+    worst = {}
+    for i in sorted({0, int(np.argmax(valid)), int(np.argmin(valid))}):
+        one = slice(i, i + 1)
+        alone = model.forward_batch(ids[one], valid[one], pos[one], mask[one], qtype[one])
+        again = model.forward_batch(ids[one], valid[one], pos[one], mask[one], qtype[one])
+        for f in fields:
+            assert np.array_equal(getattr(alone, f), getattr(again, f)), f
+            _compare("act_features" if f == "features" else f, getattr(alone, f)[0], getattr(batch, f)[i], worst)
+    print({k: f"{a:.1e}/{r:.1e}" for k, (a, r) in worst.items()}, flush=True)
