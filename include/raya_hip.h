@@ -195,6 +195,25 @@ typedef struct raya_gemm_epilogue {
     const float *bias;     /* device [n] ([2n] for GEGLU) or NULL */
     const float *residual; /* device [m][ldr] or NULL; may alias out when ldr == ldo */
     int64_t ldr;
+    /* Residual + LayerNorm across two GEMMs, the pre-LN encoder's
+     * h += x Wo^T; LayerNorm(h) Wi^T (crates/raya-core/src/encoder.rs:127-146, whose
+     * ops::layer_norm, ops.rs:51-74, is a pass of its own there):
+     *  - out_row_stats: device [m][n / 64][4] floats or NULL.  Per row and 64-column chunk
+     *    of out (after the residual add), the statistics raya_row_norm_stats turns into
+     *    the row's LayerNorm mean and 1 / sqrt(var + eps).  n a multiple of 64; not GEGLU.
+     *  - in_row_stats: device [m][4] floats (raya_row_norm_stats' output) or NULL.  The
+     *    rows of a are normalised before the product: out = epilogue(LayerNorm(a) b^T),
+     *    with b the weight whose columns the caller has multiplied by the norm's gain
+     *    (b[j][t] = gain[t] W[j][t]) and in_weight_sums its row sums (raya_weight_row_sums,
+     *    device [n], [2n] for GEGLU); a norm bias beta enters as the GEMM bias W beta.  A
+     *    row whose mean lies more than one standard deviation from zero is centred before
+     *    the contraction, as ops::layer_norm subtracts the mean before scaling; for the
+     *    others the mean comes out afterwards through the row sums.
+     * Both need the ring kernel: k a multiple of 16, lda, ldb, ldo (and ldr) multiples of
+     * 4 floats, 16-byte aligned a, b and out (and residual); otherwise RAYA_ERR_UNSUPPORTED. */
+    float *out_row_stats;
+    const float *in_row_stats;
+    const float *in_weight_sums;
 } raya_gemm_epilogue;
 
 /* Device-pointer GEMM with a fused epilogue (ep may be NULL: plain product),
@@ -204,6 +223,19 @@ typedef struct raya_gemm_epilogue {
 int raya_matmul_nt_device(float *out, int64_t ldo, const float *a, int64_t lda, const float *b,
                           int64_t ldb, uint64_t m, uint64_t n, uint64_t k,
                           const raya_gemm_epilogue *ep, void *stream);
+
+/* Each row's LayerNorm statistics (mean and 1 / sqrt(var + eps), var the biased variance,
+ * in f64 as ops::layer_norm computes them, crates/raya-core/src/ops.rs:51-74) from the
+ * chunk statistics a GEMM wrote to out_row_stats for an output of width n (a multiple of
+ * 64): chunk_stats [rows][n / 64][4] -> row_stats [rows][4], both device, for a later
+ * GEMM's in_row_stats.  eps finite and >= 0.  Asynchronous on `stream`. */
+int raya_row_norm_stats(const float *chunk_stats, uint64_t rows, uint64_t n, float eps, float *row_stats,
+                        void *stream);
+
+/* sums[j] = sum_t b[j][t] over t < k, in f64 rounded once to f32, for j < rows: the weight
+ * row sums a GEMM with in_row_stats needs (computed once per folded weight).  Device
+ * pointers, ldb >= k floats; asynchronous on `stream`. */
+int raya_weight_row_sums(const float *b, int64_t ldb, uint64_t rows, uint64_t k, float *sums, void *stream);
 
 /* ---- A post-LN encoder layer ----------------------------------------------------------------
  *

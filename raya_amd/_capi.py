@@ -49,7 +49,9 @@ class AttnBatchC(ctypes.Structure):
 
 class GemmEpilogueC(ctypes.Structure):
     _fields_ = [("activation", ctypes.c_int32), ("reserved", ctypes.c_int32),
-                ("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64)]
+                ("bias", ctypes.c_void_p), ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64),
+                ("out_row_stats", ctypes.c_void_p), ("in_row_stats", ctypes.c_void_p),
+                ("in_weight_sums", ctypes.c_void_p)]
 
 
 class ParamEntryC(ctypes.Structure):
@@ -123,6 +125,8 @@ SIGNATURES = [
     ("raya_matmul_nt", ctypes.c_int, [_vp, _sz, _vp, _sz, _vp, _sz, _u64, _u64, _u64]),
     ("raya_matmul_nt_device", ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _u64, _u64, _u64,
                                              ctypes.POINTER(GemmEpilogueC), _vp]),
+    ("raya_row_norm_stats", ctypes.c_int, [_vp, _u64, _u64, ctypes.c_float, _vp, _vp]),
+    ("raya_weight_row_sums", ctypes.c_int, [_vp, _i64, _u64, _u64, _vp, _vp]),
     ("raya_postln_workspace_bytes", ctypes.c_uint64, [ctypes.POINTER(PostLNLayerC)]),
     ("raya_postln_layer_forward", ctypes.c_int, [ctypes.POINTER(PostLNLayerC), _vp, _vp, _vp, _vp, _u64, _vp]),
     ("raya_model_load", ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_vp)]),

@@ -453,8 +453,51 @@ int raya_matmul_nt_device(float *out, int64_t ldo, const float *a, int64_t lda, 
     g.bias = ep ? ep->bias : nullptr;
     g.residual = ep ? ep->residual : nullptr;
     g.ldr = ep ? ep->ldr : 0;
+    g.out_stats = ep ? (float4 *)ep->out_row_stats : nullptr;
+    g.in_stats = ep ? (const float4 *)ep->in_row_stats : nullptr;
+    g.colsum = ep ? ep->in_weight_sums : nullptr;
+    if (g.in_stats && !g.colsum)
+        return fail(RAYA_ERR_SHAPE, "invalid shape: in_row_stats needs in_weight_sums (raya_weight_row_sums)");
+    if (g.out_stats || g.in_stats) {
+        const auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+        const bool ring = k > 0 && k % 16 == 0 && lda % 4 == 0 && ldb % 4 == 0 && ldo % 4 == 0 && al(a) &&
+                          al(b) && al(out) && (!g.residual || (g.ldr % 4 == 0 && al(g.residual)));
+        if (!ring)
+            return fail(RAYA_ERR_UNSUPPORTED,
+                        "unsupported: row statistics need k a multiple of 16 and 16-byte aligned rows");
+        if (g.out_stats && (act == RAYA_EPI_GEGLU || n % 64 != 0))
+            return fail(RAYA_ERR_UNSUPPORTED,
+                        "unsupported: out_row_stats needs n a multiple of 64 and no GEGLU epilogue");
+        if (!al(g.out_stats) || !al(g.in_stats) || ((uintptr_t)g.colsum & 3))
+            return fail(RAYA_ERR_SHAPE, "invalid shape: row statistics must be 16-byte aligned");
+    }
     const hipError_t e = launch_gemm(g, (hipStream_t)stream);
     if (e != hipSuccess) return fail_device(e, "gemm launch");
+    return ok();
+}
+
+int raya_weight_row_sums(const float *b, int64_t ldb, uint64_t rows, uint64_t k, float *sums, void *stream) {
+    if (rows > 0x7fffffffu || k > 0x7fffffffu) return fail(RAYA_ERR_UNSUPPORTED, "unsupported: dimension above 2^31");
+    if (ldb < (int64_t)k) return fail(RAYA_ERR_SHAPE, "invalid shape: ldb is smaller than k");
+    if (rows == 0) return ok();
+    if (!sums || (k > 0 && !b)) return fail(RAYA_ERR_SHAPE, "invalid shape: null device pointer");
+    const hipError_t e = launch_row_sums(b, ldb, (int)rows, (int)k, sums, (hipStream_t)stream);
+    if (e != hipSuccess) return fail_device(e, "row sums launch");
+    return ok();
+}
+
+int raya_row_norm_stats(const float *chunk_stats, uint64_t rows, uint64_t n, float eps, float *row_stats,
+                        void *stream) {
+    if (n == 0 || n % 64 != 0) return fail(RAYA_ERR_UNSUPPORTED, "unsupported: row width %llu is not a multiple of 64",
+                                           (unsigned long long)n);
+    if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(RAYA_ERR_SHAPE, "invalid shape: eps must be finite and >= 0");
+    if (rows > 0x7fffffffu || n / 64 > 0x7fffffffu)
+        return fail(RAYA_ERR_UNSUPPORTED, "unsupported: row statistics above 2^31 rows");
+    if (rows == 0) return ok();
+    if (!chunk_stats || !row_stats) return fail(RAYA_ERR_SHAPE, "invalid shape: null device pointer");
+    const hipError_t e = launch_ln_stats((const float4 *)chunk_stats, (int)rows, (int)(n / 64), eps,
+                                         (float4 *)row_stats, (hipStream_t)stream);
+    if (e != hipSuccess) return fail_device(e, "row statistics launch");
     return ok();
 }
 

@@ -213,28 +213,52 @@ unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per)
 
 namespace {
 
-// The pre-LN LayerNorm statistics of each row from its 64-column chunk (mean, M2)
-// pairs (Chan et al.'s pairwise combination, in f64, as ops::layer_norm keeps its
-// statistics in f64): (mean, 1 / sqrt(var + eps)), var the biased variance.
-__global__ void ln_stats_kernel(const float2 *chunks_in, int rows, int chunks, float eps, float2 *out) {
+// The pre-LN LayerNorm statistics of each row from its 64-column chunks'
+// (c, r = sum (x - c), s = sum (x - c)^2), in f64 as ops::layer_norm keeps its
+// statistics (crates/raya-core/src/ops.rs:51-74): a chunk's mean is c + r / 64 and
+// its sum of squared deviations s - r^2 / 64; the chunks combine as Chan et al.'s
+// pairwise update.  Out: (mean_hi, mean_lo, 1 / sqrt(var + eps), 0) with var the
+// biased variance and mean_hi + mean_lo the f64 mean to 48 bits.
+__global__ void ln_stats_kernel(const float4 *chunks_in, int rows, int chunks, float eps, float4 *out) {
     const int row = blockIdx.x * blockDim.x + threadIdx.x;
     if (row >= rows) return;
-    const float2 *st = chunks_in + (int64_t)row * chunks;
+    const float4 *st = chunks_in + (int64_t)row * chunks;
     double mean = 0.0;
-    for (int c = 0; c < chunks; ++c) mean += st[c].x;
+    for (int c = 0; c < chunks; ++c) mean += (double)st[c].x + (double)st[c].y * (1.0 / 64.0);
     mean /= chunks;
     double m2 = 0.0;
     for (int c = 0; c < chunks; ++c) {
-        const double dm = (double)st[c].x - mean;
-        m2 += (double)st[c].y + 64.0 * dm * dm;
+        const double r = st[c].y, cm = (double)st[c].x + r * (1.0 / 64.0);
+        const double dm = cm - mean;
+        m2 += ((double)st[c].z - r * r * (1.0 / 64.0)) + 64.0 * dm * dm;
     }
-    const double var = m2 / (64.0 * chunks);
-    out[row] = make_float2((float)mean, (float)(1.0 / sqrt(var + (double)eps)));
+    const double var = fmax(m2, 0.0) / (64.0 * chunks);
+    const float hi = (float)mean;
+    out[row] = make_float4(hi, (float)(mean - (double)hi), (float)(1.0 / sqrt(var + (double)eps)), 0.0f);
+}
+
+// One wave per row: each lane sums a strided share of the row in f64, then the
+// lanes' sums are combined by a fixed butterfly (the same order every call).
+__global__ void row_sums_kernel(const float *b, int64_t ldb, int rows, int k, float *sums) {
+    const int row = blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *p = b + (int64_t)row * ldb;
+    double s = 0.0;
+    for (int t = lane; t < k; t += 64) s += (double)p[t];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) sums[row] = (float)s;
 }
 
 }  // namespace
 
-hipError_t launch_ln_stats(const float2 *chunks, int rows, int n_chunks, float eps, float2 *out, hipStream_t stream) {
+hipError_t launch_row_sums(const float *b, int64_t ldb, int rows, int k, float *sums, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(row_sums_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, b, ldb, rows, k, sums);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_stats(const float4 *chunks, int rows, int n_chunks, float eps, float4 *out, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(ln_stats_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, stream, chunks, rows,
                        n_chunks, eps, out);

@@ -22,6 +22,8 @@
 // also apply rotary embedding (ops.rs:118-141) to the q and k sections of a
 // packed QKV projection, so encoder::attend's split_qkv + rope_in_place pass
 // (encoder.rs:36-71) is not needed.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace raya {
@@ -260,9 +262,11 @@ __device__ __forceinline__ void dma16(const float *src, uint32_t lds_addr) {
 __device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
 
 // Sum over each 16-lane row of the wave with DPP moves (no LDS crossbar): lane
-// pairs (quad_perm [1,0,3,2]), quads ([2,3,0,1]), then the row's four quads by
-// rotating it 4 and 8 lanes.  Lanes of a row may differ in the last bit (their
-// quad sums are added in different orders).
+// pairs (quad_perm [1,0,3,2]), quads ([2,3,0,1]), then the row's halves of 8
+// (row_half_mirror pairs quad 0 with 1 and 2 with 3) and the row (row_mirror
+// pairs quad 0 with 3 and 1 with 2).  Every step adds the same two values in
+// each lane of a pair, in the other order, and addition commutes, so all 16
+// lanes hold the same bits.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
@@ -270,8 +274,8 @@ __device__ __forceinline__ float dpp(float x) {
 __device__ __forceinline__ float row16_sum(float x) {
     x += dpp<0xB1>(x);   // quad_perm [1, 0, 3, 2]
     x += dpp<0x4E>(x);   // quad_perm [2, 3, 0, 1]
-    x += dpp<0x124>(x);  // row_ror 4
-    x += dpp<0x128>(x);  // row_ror 8
+    x += dpp<0x141>(x);  // row_half_mirror
+    x += dpp<0x140>(x);  // row_mirror
     return x;
 }
 
@@ -288,14 +292,17 @@ constexpr int kStageStrideGlu = 40;   // 32 GeGLU output columns per wave
 constexpr int kStageFloats = 32 * kStageStride;  // per wave: 32 rows at a time
 
 //
-// With g.in_stats, rowstat holds (mean, rstd) of the workgroup's 128 input rows
-// and the accumulators are normalised first (see GemmLaunch).  With
-// g.out_stats, each wave's 64 output columns are one chunk: the 16 lanes that
-// hold a row reduce its sum, then its squared deviations from the chunk mean.
+// With g.in_stats, rownorm holds (rest, rstd) of the workgroup's 128 input rows,
+// rest = (mean_hi - centre) + mean_lo the part of the mean the centring left (see
+// norm_centre), and the accumulators are normalised first: y = rstd (acc - rest
+// colsum).  With g.out_stats, each
+// wave's 64 output columns are one chunk: the 16 lanes that hold a row reduce
+// its sum to the chunk mean c (the same bits in every lane), then the deviations
+// from c and their squares.
 template <int ACT, bool ROPE, bool NORM, bool STATS>
 __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&acc)[2][2], int m0, int n0,
                                                 int wm, int wn, int li, int h, int lane, float *stg,
-                                                const float2 *rowstat, const float (&cs)[2]) {
+                                                const float2 *rownorm, const float (&cs)[2]) {
     constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
     constexpr int COLS = GEGLU ? 32 : 64;  // output columns of this wave
     constexpr int S = GEGLU ? kStageStrideGlu : kStageStride;
@@ -306,7 +313,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float2 st = rowstat[wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3)];
+                const float2 st = rownorm[wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3)];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j][r] = st.y * (acc[i][j][r] - st.x * cs[j]);
             }
@@ -381,15 +388,28 @@ __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&
                 // n is a multiple of 64, so this wave's 64 columns are either all in range
                 // (a chunk of the row) or all past n (a tile wider than the matrix: no chunk).
                 if (c0 < g.n) {
-                    const float mean = row16_sum((v.x + v.y) + (v.z + v.w)) * (1.0f / 64.0f);
-                    const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
-                    const float m2 = row16_sum((dx * dx + dy * dy) + (dz * dz + dw * dw));
-                    if (c4 == 0 && row < g.m) g.out_stats[(int64_t)row * (g.n / 64) + (c0 >> 6)] = make_float2(mean, m2);
+                    const float c = row16_sum((v.x + v.y) + (v.z + v.w)) * (1.0f / 64.0f);
+                    const float dx = v.x - c, dy = v.y - c, dz = v.z - c, dw = v.w - c;
+                    const float r1 = row16_sum((dx + dy) + (dz + dw));
+                    const float r2 = row16_sum((dx * dx + dy * dy) + (dz * dz + dw * dw));
+                    if (c4 == 0 && row < g.m)
+                        g.out_stats[(int64_t)row * (g.n / 64) + (c0 >> 6)] = make_float4(c, r1, r2, 0.0f);
                 }
             }
         }
     }
 }
+
+// The folded LayerNorm's centre of an input row with statistics st = (mean_hi,
+// mean_lo, rstd, 0): the row's A operands enter the product as x - centre.  A row
+// within one standard deviation of zero (|mean| rstd <= 1) is not centred: the
+// mean comes out afterwards as mean colsum, whose cancellation then costs at most
+// about as much as the product's own rounding (mean_lo, below half a unit of
+// mean_hi, is dropped there).  Rows further out are centred by mean_hi (exact for
+// x within a factor 2 of it), so that only mean_lo colsum is subtracted
+// afterwards.  A function of the row alone: a row's result does not depend on the
+// rows it shares a workgroup with.
+__device__ __forceinline__ float norm_centre(float4 st) { return fabsf(st.x) * st.z > 1.0f ? st.x : 0.0f; }
 
 // NORM: the input rows' LayerNorm is folded in (GemmLaunch::in_stats); STATS:
 // the output rows' chunk statistics are written (GemmLaunch::out_stats).
@@ -417,22 +437,16 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
 
     // This thread's DMA sources: slot q = (2 wave + j) 64 + lane holds stored
     // chunk q % 4 of tile row q / 4, i.e. data chunk (q % 4) ^ rswz(row).
-    // The input rows' (mean, rstd), one row per thread of the first half, loaded
-    // before the K loop and used after it.
-    // The weight rows' sums this lane's columns need (GemmLaunch::colsum), likewise.
-    float2 my_rowstat = make_float2(0.f, 0.f);
-    float cs[2] = {0.f, 0.f};
+    // Folded LayerNorm: the centres of the two A rows this lane reads out of LDS
+    // (rows wm + li and wm + 32 + li of the tile).  The subtraction runs only in
+    // workgroups where some row is centred (subtracting a centre of 0 is exact, so
+    // the other rows are unchanged).
+    float cen[2] = {0.f, 0.f};
+    bool centre = false;
     if constexpr (NORM) {
-        if (tid < BM) my_rowstat = g.in_stats[min(m0 + tid, g.m - 1)];
-        const int c0 = n0 + (GEGLU ? (wn >> 1) : wn);
-        if constexpr (GEGLU) {
-            const int col = min(c0 + li, g.n - 1);
-            cs[0] = g.colsum[col];
-            cs[1] = g.colsum[g.n + col];
-        } else {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) cs[j] = g.colsum[min(c0 + 32 * j + li, g.n - 1)];
-        }
+        for (int i = 0; i < 2; ++i) cen[i] = norm_centre(g.in_stats[min(m0 + wm + 32 * i + li, g.m - 1)]);
+        centre = __builtin_amdgcn_readfirstlane(__syncthreads_or(cen[0] != 0.f || cen[1] != 0.f)) != 0;
     }
 
     const float *asrc[2], *bsrc[2];
@@ -502,6 +516,10 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
             x[r + 3] = t[q].w;
         }
     } else {
+      // The K loop, with (C) or without the A operands' centring: two copies, so that
+      // the one without runs the plain kernel's schedule.
+      const auto kloop = [&](auto centre_tag) {
+        constexpr bool C = decltype(centre_tag)::value;
         issue(0, 0);
         if (nk > 1) issue(1, 1);
         int stage = 0;
@@ -530,6 +548,12 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
                     const int ra = wm + 32 * i + li, rb = wn + 32 * i + li;
                     av[i] = *(const float4 *)&As[ra * RBK + 4 * ((kc + h) ^ rswz(ra))];
                     bv[i] = *(const float4 *)&Bs[rb * RBK + 4 * ((kc + h) ^ rswz(rb))];
+                    if constexpr (C) {
+                        av[i].x -= cen[i];
+                        av[i].y -= cen[i];
+                        av[i].z -= cen[i];
+                        av[i].w -= cen[i];
+                    }
                 }
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
@@ -540,6 +564,15 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
             }
             __builtin_amdgcn_s_setprio(0);
             stage = stage == RSTAGES - 1 ? 0 : stage + 1;
+        }
+      };
+        if constexpr (NORM) {
+            if (centre)
+                kloop(std::true_type{});
+            else
+                kloop(std::false_type{});
+        } else {
+            kloop(std::false_type{});
         }
         if (S > 1) {
             // The partial tile goes out in the accumulator layout (each wave's 64 x 64 quadrant
@@ -558,13 +591,29 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
                          (!g.residual || ((g.ldr & 3) == 0 && ((uintptr_t)g.residual & 15) == 0));
     if (vec_out) {
         __syncthreads();  // every wave's reads of the last slab are done: the ring is free
-        float2 *rowstat = (float2 *)(ring + 4 * kStageFloats);
+        // Folded LayerNorm: one row's (rest, rstd) per thread of the first half and the
+        // weight rows' sums this lane's columns need (GemmLaunch::colsum), read after the
+        // K loop so that they hold no registers there.
+        float2 *rownorm = (float2 *)(ring + 4 * kStageFloats);
+        float cs[2] = {0.f, 0.f};
         if constexpr (NORM) {
-            if (tid < BM) rowstat[tid] = my_rowstat;
+            if (tid < BM) {
+                const float4 st = g.in_stats[min(m0 + tid, g.m - 1)];
+                rownorm[tid] = make_float2((st.x - norm_centre(st)) + st.y, st.z);
+            }
+            const int c0 = n0 + (GEGLU ? (wn >> 1) : wn);
+            if constexpr (GEGLU) {
+                const int col = min(c0 + li, g.n - 1);
+                cs[0] = g.colsum[col];
+                cs[1] = g.colsum[g.n + col];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) cs[j] = g.colsum[min(c0 + 32 * j + li, g.n - 1)];
+            }
             __syncthreads();
         }
         epilogue_staged<ACT, ROPE, NORM, STATS>(g, acc, m0, n0, wm, wn, li, h, lane, ring + wave * kStageFloats,
-                                                rowstat, cs);
+                                                rownorm, cs);
     } else {
         epilogue<ACT, ROPE>(g, acc, m0, n0, wm, wn, li, h);
     }

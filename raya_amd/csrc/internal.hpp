@@ -59,16 +59,23 @@ struct GemmLaunch {
     const int32_t *positions;
     int32_t rope_cols;
     // A pre-LN LayerNorm of the input rows folded into the product (the ring
-    // kernel's staged epilogue only): b holds the weight with the norm's gain
-    // folded into its columns, colsum[j] = sum_t b[j][t], and in_stats each row's
-    // (mean, 1 / sqrt(var + eps)) ([m], from launch_ln_stats); then
-    //   y = rstd(row) * (acc - mean(row) * colsum[j])
-    // before bias, activation and RoPE, which is LayerNorm(a) @ W^T.  Null: off.
-    const float2 *in_stats;
+    // kernel only): b holds the weight with the norm's gain folded into its
+    // columns, colsum[j] = sum_t b[j][t] (f64, rounded), and in_stats each row's
+    // (mean_hi, mean_lo, rstd, 0) ([m], from launch_ln_stats; mean = mean_hi +
+    // mean_lo, rstd = 1 / sqrt(var + eps)).  A row whose mean is more than one
+    // standard deviation from zero has its A operands centred by mean_hi as they
+    // leave LDS, so that its mean is removed before the contraction as
+    // ops::layer_norm removes it before scaling; the rest of the mean comes out
+    // as mean colsum.  Then y = rstd (acc - mean' colsum) before bias, activation
+    // and RoPE: LayerNorm(a) W^T.  Null: off.
+    const float4 *in_stats;
     const float *colsum;
-    // (mean, M2) of each output row over each 64-column chunk, after the
-    // residual add ([m][n / 64]); n a multiple of 64.  Null: off.
-    float2 *out_stats;
+    // Per output row and 64-column chunk, after the residual add ([m][n / 64]; n a
+    // multiple of 64): (c, sum (x - c), sum (x - c)^2, 0) with c the chunk's f32
+    // mean, the same c in every lane, so that launch_ln_stats recovers the chunk's
+    // mean as c + sum (x - c) / 64 to the precision of the deviations rather than
+    // of |x|.  Null: off.
+    float4 *out_stats;
     // Split-K (the ring kernel only), for launches whose output tiles alone leave
     // compute units idle: each tile's K loop is divided among `splits` workgroups,
     // which store their partial tiles to `partials` ([tiles][splits][128 x 128]);
@@ -109,9 +116,11 @@ struct LayerNormLaunch {
 };
 
 hipError_t launch_layer_norm(const LayerNormLaunch &l, hipStream_t stream);
-// Each row's (mean, 1 / sqrt(var + eps)) from its 64-column chunk statistics
-// (GemmLaunch::out_stats, [rows][n_chunks]) into out ([rows]).
-hipError_t launch_ln_stats(const float2 *chunks, int rows, int n_chunks, float eps, float2 *out, hipStream_t stream);
+// Each row's (mean_hi, mean_lo, 1 / sqrt(var + eps), 0) from its 64-column chunk
+// statistics (GemmLaunch::out_stats, [rows][n_chunks]) into out ([rows]).
+hipError_t launch_ln_stats(const float4 *chunks, int rows, int n_chunks, float eps, float4 *out, hipStream_t stream);
+// sums[j] = sum over t < k of b[j][t] in f64, rounded to f32 ([rows]).
+hipError_t launch_row_sums(const float *b, int64_t ldb, int rows, int k, float *sums, hipStream_t stream);
 hipError_t launch_rope(float *qkv, int64_t ld, const int32_t *positions, const float *cos_t,
                        const float *sin_t, int rows, int d, int head_dim, hipStream_t stream);
 hipError_t launch_gather_rows(const float *h, int64_t ldh, const int32_t *rows, int n, int d,

@@ -578,7 +578,7 @@ void rope_table(float theta, int head_dim, int positions, std::vector<float> &co
 
 // The encoder's pre-LN LayerNorms folded into the GEMMs that read them (GemmLaunch::in_stats):
 // per layer, Wqkv (layers >= 1, after attn_norm) and Wi (after mlp_norm) with the norm's gain
-// multiplied into their columns, and each weight row's sum.  Offsets in floats into `buf`.
+// multiplied into their columns, and each folded weight row's sum.  Offsets in floats into `buf`.
 struct FoldedNorms {
     DeviceBuf buf;
     std::vector<size_t> qkv, qkv_sum, wi, wi_sum;
@@ -646,55 +646,68 @@ int ensure_act_weight(const Model &m, DeviceModel &dm, uint64_t ld_act) {
     return RAYA_OK;
 }
 
-// The folding is exact algebra: LN(x) W^T = rstd (x - mean) (g * W)^T with g the norm's gain,
-// i.e. rstd (x (g * W)^T - mean colsum).  Built on the host once per device (the products
-// g_t W[j][t] in f32, the row sums in f64), only when every chunk of a row is whole.
-bool norms_foldable(const Config &c) { return c.hidden % 64 == 0; }
+// LN(x) W^T = rstd ((x - c) (g * W)^T - (mean - c) colsum) with g the norm's gain, colsum[j]
+// the row sums of g * W and c a per-row centre (0, or the mean's leading part for rows far
+// from zero; GemmLaunch::in_stats).  Built on the host once per device: the products
+// g_t W[j][t] in f32 (as LN's output times W rounds them) and their row sums in f64.  The
+// residual GEMMs that produce the statistics need whole 64-column chunks (hidden a multiple of
+// 64) and the ring kernel (every GEMM depth a multiple of 16: hidden and the MLP's intermediate
+// size); other shapes keep the LayerNorm kernels.
+bool norms_foldable(const Config &c) { return c.hidden % 64 == 0 && c.inter % 16 == 0; }
 
 int ensure_folded(const Model &m, DeviceModel &dm) {
     const Config &c = m.cfg;
     if (!dm.folded.qkv.empty() || !norms_foldable(c)) return RAYA_OK;
     const uint64_t d = c.hidden, n3 = 3 * d, n2 = 2 * c.inter;
     std::vector<float> host;
-    host.reserve((size_t)c.layers * (n3 * d + n3 + n2 * d + n2));
-    FoldedNorms &f = dm.folded;
+    host.reserve((size_t)c.layers * (n3 + n2) * (d + 1));
+    FoldedNorms f;
+    std::vector<float> sums;
+    // Appends the folded block (rows x d) and then its row sums; blocks stay 16-byte aligned
+    // because d and every row count here are multiples of 4.
     auto fold = [&](const std::string &w, const std::string &gain, uint64_t rows, std::vector<size_t> &off,
-                    std::vector<size_t> &off_sum) {
-        const float *wp = m.w.host.data() + m.w.entries[m.w.index.at(w)].offset;
-        const float *gp = m.w.host.data() + m.w.entries[m.w.index.at(gain)].offset;
+                    std::vector<size_t> &off_sum) -> int {
+        const auto iw = m.w.index.find(w), ig = m.w.index.find(gain);
+        if (iw == m.w.index.end() || ig == m.w.index.end())
+            return fail(RAYA_ERR_WEIGHTS, "missing %s", (iw == m.w.index.end() ? w : gain).c_str());
+        const float *wp = m.w.host.data() + m.w.entries[iw->second].offset;
+        const float *gp = m.w.host.data() + m.w.entries[ig->second].offset;
         off.push_back(host.size());
-        for (uint64_t j = 0; j < rows; ++j)
-            for (uint64_t t = 0; t < d; ++t) host.push_back(wp[j * d + t] * gp[t]);
-        off_sum.push_back(host.size());
-        const float *fw = host.data() + off.back();
+        sums.assign(rows, 0.0f);
         for (uint64_t j = 0; j < rows; ++j) {
             double sum = 0.0;
-            for (uint64_t t = 0; t < d; ++t) sum += fw[j * d + t];
-            host.push_back((float)sum);
+            for (uint64_t t = 0; t < d; ++t) {
+                const float x = wp[j * d + t] * gp[t];
+                host.push_back(x);
+                sum += x;
+            }
+            sums[j] = (float)sum;
         }
+        off_sum.push_back(host.size());
+        host.insert(host.end(), sums.begin(), sums.end());
+        return RAYA_OK;
     };
     for (uint64_t i = 0; i < c.layers; ++i) {
         const std::string p = "encoder.layers." + std::to_string(i);
+        int rc = RAYA_OK;
         if (i > 0) {
-            fold(p + ".attn.Wqkv.weight", p + ".attn_norm.weight", n3, f.qkv, f.qkv_sum);
-        } else {
+            rc = fold(p + ".attn.Wqkv.weight", p + ".attn_norm.weight", n3, f.qkv, f.qkv_sum);
+        } else {  // layer 0 has no attn_norm
             f.qkv.push_back(0);
             f.qkv_sum.push_back(0);
         }
-        fold(p + ".mlp.Wi.weight", p + ".mlp_norm.weight", n2, f.wi, f.wi_sum);
+        if (!rc) rc = fold(p + ".mlp.Wi.weight", p + ".mlp_norm.weight", n2, f.wi, f.wi_sum);
+        if (rc) return rc;
     }
-    // An empty f.qkv means "not built": on a failure the offsets are cleared, so the next
-    // call builds again.
-    int rc = f.buf.reserve(host.size() * sizeof(float));
-    hipError_t e = rc ? hipSuccess
-                      : hipMemcpy(f.buf.ptr, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
-    if (rc || e != hipSuccess) {
-        f.qkv.clear();
-        f.qkv_sum.clear();
-        f.wi.clear();
-        f.wi_sum.clear();
-        return rc ? rc : fail_device(e, "upload folded norm weights");
-    }
+    // Empty offsets mean "not built": they are set only once the upload has succeeded.
+    int rc = dm.folded.buf.reserve(host.size() * sizeof(float));
+    if (rc) return rc;
+    const hipError_t e = hipMemcpy(dm.folded.buf.ptr, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return fail_device(e, "upload folded norm weights");
+    dm.folded.qkv = std::move(f.qkv);
+    dm.folded.qkv_sum = std::move(f.qkv_sum);
+    dm.folded.wi = std::move(f.wi);
+    dm.folded.wi_sum = std::move(f.wi_sum);
     return RAYA_OK;
 }
 
@@ -966,8 +979,8 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
         probe.take<float>(B * ld_act);   // act input, rows padded to the act head's depth
         probe.take<float>(B * 256);      // act hidden
         probe.take<float>(B * nact);     // act logits
-        probe.take<float>(T * (d / 64) * 2);  // LayerNorm chunk statistics of h
-        probe.take<float>(T * 2);             // and each row's (mean, rstd)
+        probe.take<float4>(T * (d / 64));   // LayerNorm chunk statistics of h
+        probe.take<float4>(T);              // and each row's (mean_hi, mean_lo, rstd)
         probe.take<float>(split_cap);         // split-K partial tiles
         need = probe.off;
     }
@@ -984,8 +997,8 @@ int raya_model_forward(raya_model *model, const raya_forward_batch *in, raya_for
     float *d_feat = cv.take<float>(B * 4), *d_pooled = cv.take<float>(B * d);
     float *act_in = cv.take<float>(B * ld_act), *act_hid = cv.take<float>(B * 256);
     float *d_act = cv.take<float>(B * nact);
-    float2 *hstats = (float2 *)cv.take<float>(T * (d / 64) * 2);
-    float2 *hrow = (float2 *)cv.take<float>(T * 2);
+    float4 *hstats = cv.take<float4>(T * (d / 64));
+    float4 *hrow = cv.take<float4>(T);
     float *partials = cv.take<float>(split_cap);
     const int32_t *d_ids = d_ints + o_ids, *d_pos = d_ints + o_pos, *d_rowseq = d_ints + o_rs;
     const int32_t *d_start = d_ints + o_start, *d_valid = d_ints + o_valid, *d_qtype = d_ints + o_q;

@@ -363,10 +363,16 @@ class HipGemm(GemmBackend):
             _raise_last(rc)
 
     def matmul_nt_device(self, out, a, b, *, bias=None, activation: int = C.RAYA_EPI_NONE,
-                         residual=None, stream=None) -> None:
+                         residual=None, out_row_stats=None, in_row_stats=None, in_weight_sums=None,
+                         stream=None) -> None:
         """out[m, n] = act(a[m, k] @ b[n, k]^T + bias) + residual on GPU tensors.
         For GEGLU, b is [2n, k] and bias [2n].  Row strides are taken from the
-        tensors (last dimension must be contiguous)."""
+        tensors (last dimension must be contiguous).
+
+        out_row_stats ([m, n // 64, 4] float32): the chunk statistics of out for
+        row_norm_stats.  in_row_stats ([m, 4], from row_norm_stats) with in_weight_sums
+        (b's row sums, from weight_row_sums): a's rows are LayerNorm-ed before the
+        product, b carrying the norm's gain in its columns."""
         import torch
 
         # Every operand is checked before anything reaches the device: another
@@ -374,7 +380,10 @@ class HipGemm(GemmBackend):
         # than it reads, or a pointer it cannot read.  Shapes and dtypes first,
         # the device last.
         named = [("out", out), ("a", a), ("b", b)]
-        named += [(n_, t) for n_, t in (("bias", bias), ("residual", residual)) if t is not None]
+        named += [(n_, t) for n_, t in (("bias", bias), ("residual", residual),
+                                        ("out_row_stats", out_row_stats), ("in_row_stats", in_row_stats),
+                                        ("in_weight_sums", in_weight_sums))
+                  if t is not None]
         for name, t in named:
             if not isinstance(t, torch.Tensor):
                 raise TypeError(f"`{name}` must be a torch tensor")
@@ -393,16 +402,68 @@ class HipGemm(GemmBackend):
         if residual is not None and (residual.dim() != 2 or tuple(residual.shape) != (m, n)
                                      or residual.stride(1) != 1):
             raise ShapeError("invalid shape: `residual` must be [m, n] with contiguous rows")
+        if out_row_stats is not None and (not out_row_stats.is_contiguous()
+                                          or tuple(out_row_stats.shape) != (m, n // 64, 4)):
+            raise ShapeError(f"invalid shape: `out_row_stats` must be a contiguous [{m}, {n // 64}, 4]")
+        if in_row_stats is not None and (not in_row_stats.is_contiguous()
+                                         or tuple(in_row_stats.shape) != (m, 4)):
+            raise ShapeError(f"invalid shape: `in_row_stats` must be a contiguous [{m}, 4]")
+        if in_weight_sums is not None and (in_weight_sums.dim() != 1 or in_weight_sums.numel() != rows_b
+                                           or not in_weight_sums.is_contiguous()):
+            raise ShapeError(f"invalid shape: `in_weight_sums` must be a contiguous vector of {rows_b} entries")
         for name, t in named:
             if not t.is_cuda:
                 raise TypeError(f"`{name}` must be a torch tensor on the GPU")
         ep = C.GemmEpilogueC(activation, 0,
                              _dev_ptr(bias, "bias") if bias is not None else None,
                              _dev_ptr(residual, "residual") if residual is not None else None,
-                             residual.stride(0) if residual is not None else 0)
+                             residual.stride(0) if residual is not None else 0,
+                             _dev_ptr(out_row_stats, "out_row_stats") if out_row_stats is not None else None,
+                             _dev_ptr(in_row_stats, "in_row_stats") if in_row_stats is not None else None,
+                             _dev_ptr(in_weight_sums, "in_weight_sums") if in_weight_sums is not None else None)
         rc = C.lib().raya_matmul_nt_device(_dev_ptr(out, "out"), out.stride(0), _dev_ptr(a, "a"),
                                            a.stride(0), _dev_ptr(b, "b"), b.stride(0), m, n, k,
                                            ctypes.byref(ep), _stream_ptr(stream))
+        if rc:
+            _raise_last(rc)
+
+    def weight_row_sums(self, b, sums, stream=None) -> None:
+        """sums[j] = sum_t b[j, t] (f64, rounded once) on GPU tensors: the in_weight_sums of
+        a folded weight b ([rows, k], contiguous rows)."""
+        import torch
+
+        for name, t in (("b", b), ("sums", sums)):
+            if not isinstance(t, torch.Tensor) or t.dtype != torch.float32:
+                raise TypeError(f"`{name}` must be a float32 torch tensor")
+        if b.dim() != 2 or b.stride(1) != 1 or sums.dim() != 1 or sums.numel() != b.shape[0] \
+                or not sums.is_contiguous():
+            raise ShapeError("invalid shape: b [rows, k] with contiguous rows and sums [rows]")
+        for name, t in (("b", b), ("sums", sums)):
+            if not t.is_cuda:
+                raise TypeError(f"`{name}` must be a torch tensor on the GPU")
+        rc = C.lib().raya_weight_row_sums(_dev_ptr(b, "b"), b.stride(0), b.shape[0], b.shape[1],
+                                          _dev_ptr(sums, "sums"), _stream_ptr(stream))
+        if rc:
+            _raise_last(rc)
+
+    def row_norm_stats(self, chunk_stats, row_stats, eps: float, stream=None) -> None:
+        """Each row's LayerNorm (mean, 1/sqrt(var + eps)) from a GEMM's out_row_stats
+        ([m, n // 64, 4]) into row_stats ([m, 4]), for a later in_row_stats."""
+        import torch
+
+        for name, t in (("chunk_stats", chunk_stats), ("row_stats", row_stats)):
+            if not isinstance(t, torch.Tensor) or t.dtype != torch.float32:
+                raise TypeError(f"`{name}` must be a float32 torch tensor")
+            if not t.is_contiguous():
+                raise ShapeError(f"invalid shape: `{name}` must be contiguous")
+        if chunk_stats.dim() != 3 or chunk_stats.shape[2] != 4 or tuple(row_stats.shape) != (chunk_stats.shape[0], 4):
+            raise ShapeError("invalid shape: chunk_stats [m, n // 64, 4] and row_stats [m, 4]")
+        for name, t in (("chunk_stats", chunk_stats), ("row_stats", row_stats)):
+            if not t.is_cuda:
+                raise TypeError(f"`{name}` must be a torch tensor on the GPU")
+        m, chunks = chunk_stats.shape[0], chunk_stats.shape[1]
+        rc = C.lib().raya_row_norm_stats(_dev_ptr(chunk_stats, "chunk_stats"), m, 64 * chunks, eps,
+                                         _dev_ptr(row_stats, "row_stats"), _stream_ptr(stream))
         if rc:
             _raise_last(rc)
 

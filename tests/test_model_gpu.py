@@ -236,11 +236,11 @@ def test_base_width_layers_match_oracle(tmp_path):
 
     The goldens' 1e-5 per stage and 1e-6 on probabilities are set for the reference's small
     fixtures (d <= 128).  At d = 768 the contractions run over 768 and 3,072 terms in another
-    order than the reference's sequential sums, so every output is held to the fp32 bar of
-    max-abs 1e-4 and rel-L2 1e-5 (measured: pooled 4e-5 max-abs, 4e-6 rel-L2; logits of
-    magnitude ~1.4 within 1e-5, i.e. about 100 units in the last place after four layers), and
-    the probabilities to what the logits' own error allows: |dp_i| <= p_i (1 - p_i)
-    |dz_i - dz_j| <= max|dz| / 2 (measured 2e-6)."""
+    order than the reference's sequential sums, so the 768-wide outputs (pooled, act_logits)
+    are held to the fp32 bar of max-abs 1e-4 and rel-L2 1e-5 (measured: pooled 5.6e-5
+    max-abs, 5.4e-6 rel-L2; act_logits 2.3e-5), the logits (magnitude ~1.4) to the goldens'
+    1e-5 (measured 6.8e-6, about 60 units in the last place after four layers) and the
+    probabilities to 5e-6 (measured 1.3e-6: |dp_i| <= p_i (1 - p_i) |dz_i - dz_j|)."""
     cfg, cdir, w = make_model(tmp_path, 768, 12, layers=3, inter=3072, head_layers=1, vocab=500,
                               local_attention=128, seed=11)
     model = M.Model.load(cdir)
@@ -257,8 +257,8 @@ def test_base_width_layers_match_oracle(tmp_path):
             rel = float(np.sqrt((err ** 2).sum() / max((exp ** 2).sum(), 1e-30)))
             print(f"  seq {i} {name}: max-abs {err.max():.2e} rel-L2 {rel:.2e}")
             assert err.max() <= 1e-4 and rel <= 1e-5, (i, name, float(err.max()), rel)
-        dz = float(np.abs(out.logits[i] - want.logits).max())
-        assert np.abs(out.probabilities[i] - want.probabilities).max() <= dz / 2 + 1e-6, dz
+        assert np.abs(out.logits[i] - want.logits).max() <= LAYER_TOL
+        assert np.abs(out.probabilities[i] - want.probabilities).max() <= 5e-6
 
 
 @pytest.mark.parametrize("case", ["medium", "padded"])
@@ -284,3 +284,52 @@ def test_folded_norms_match_the_layernorm_kernels(case, monkeypatch):
         worst = max(worst, err)
         assert err <= tol, (name, err)
     print(f"{case}: folded vs kernel LayerNorm, worst stage difference {worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("kappa", [5.0, 50.0])
+def test_folded_norms_on_rows_far_from_zero(tmp_path, monkeypatch, kappa):
+    """Residual rows 10 and 100 sigma from zero through the folded pre-LN LayerNorms.
+
+    Every Wo gets kappa added to all its entries, so each attention output row adds the
+    same kappa * sum(ctx row) to all hidden columns: the residual stream's rows drift to
+    |mean| / sigma of about 2 kappa by the second layer (checked on the oracle's trace),
+    where a fold that removed the mean after the contraction cancels catastrophically.
+    The rank-1 term also multiplies every rounding of the context by about kappa * sqrt(d),
+    on the oracle as on the device, so the stages are held to the LayerNorm kernels' own
+    distance from the oracle (RAYA_LN_FUSION=0 on the same model): the folded path within
+    twice that distance plus one f32 unit of the stage's magnitude, at every stage, and the
+    outputs within twice that distance or the goldens' 1e-5, whichever is larger."""
+    from safetensors.numpy import save_file
+
+    cfg, cdir, w = make_model(tmp_path, 128, 2, layers=3, inter=256, head_layers=1, seed=21)
+    for i in range(cfg.layers):
+        name = f"encoder.layers.{i}.attn.Wo.weight"
+        w[name] = (w[name] + np.float32(kappa)).astype(np.float32)
+    save_file(w, os.path.join(cdir, "model.safetensors"))
+    model = M.Model.load(cdir)
+    rng = np.random.default_rng(22)
+    ids, valid, pos, mask, qtype = random_batch(rng, cfg, b=3, seq=96, k=3)
+    print(f"kappa {kappa}: valid {valid.tolist()}", flush=True)
+    fused, plain = M.Trace(), M.Trace()
+    out_f = model.forward_batch(ids, valid, pos, mask, qtype, trace=fused)
+    monkeypatch.setenv("RAYA_LN_FUSION", "0")
+    out_p = model.forward_batch(ids, valid, pos, mask, qtype, trace=plain)
+    names = [f"encoder_layer_{i:02d}" for i in range(cfg.layers)] + ["encoder_final_norm", "head_layer_00"]
+    for i in range(len(valid)):
+        v = int(valid[i])
+        want = F.forward(cfg, w, ids[i], v, pos[i], mask[i], int(qtype[i]))
+        h = want.trace["encoder_layer_01"][:v].astype(np.float64)
+        drift = float(np.median(np.abs(h.mean(1)) / h.std(1)))
+        assert drift >= kappa, drift
+        for name in names:
+            ref = want.trace[name][:v]
+            ef = float(np.abs(fused.get(name)[1][i, :v] - ref).max())
+            ep = float(np.abs(plain.get(name)[1][i, :v] - ref).max())
+            unit = float(np.spacing(np.float32(np.abs(ref).max())))
+            print(f"  seq {i} {name}: folded {ef:.2e}, LayerNorm kernels {ep:.2e} (drift {drift:.0f} sigma)")
+            assert ef <= 2 * ep + unit, (i, name, ef, ep)
+        for name in ("logits", "probabilities", "act_logits", "pooled"):
+            ef = float(np.abs(getattr(out_f, name)[i] - getattr(want, name)).max())
+            ep = float(np.abs(getattr(out_p, name)[i] - getattr(want, name)).max())
+            print(f"  seq {i} {name}: folded {ef:.2e}, LayerNorm kernels {ep:.2e}")
+            assert ef <= max(2 * ep, LAYER_TOL), (i, name, ef, ep)

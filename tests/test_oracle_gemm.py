@@ -2,6 +2,7 @@
 import math
 
 import numpy as np
+import pytest
 
 import oracle
 
@@ -89,3 +90,46 @@ def test_rope_rotate_half():
     y = oracle.rope(np.array([0, 1, 0, 0, 0, 1, 0, 0], np.float32).reshape(1, 2, 4), 10000.0).ravel()
     assert abs(y[5] - np.cos(np.float32(0.01))) < 1e-6 and abs(y[7] - np.sin(np.float32(0.01))) < 1e-6
     assert abs((x[4:] ** 2).sum() - 1) < 1e-6
+
+
+def _folded_layernorm_f32(h, w, mode: str):
+    """LayerNorm(h) W^T (gain 1) folded into one f32 product as the GEMM computes it:
+    statistics in f64 rounded to f32 (mean = hi + lo); the operands enter as h - c and the
+    rest of the mean comes out afterwards, y = rstd (acc - ((hi - c) + lo) colsum).  c = 0
+    for every row ("after"), c = hi for every row ("centre"), or the GEMM's rule ("rows"):
+    c = hi for rows with |hi| rstd > 1, else 0."""
+    h64 = h.astype(np.float64)
+    mean, rstd = h64.mean(1), (1.0 / np.sqrt(h64.var(1) + 1e-12)).astype(np.float32)
+    hi = mean.astype(np.float32)
+    lo = (mean - hi).astype(np.float32)
+    if mode == "after":
+        c = np.zeros_like(hi)
+    elif mode == "centre":
+        c = hi
+    else:
+        c = np.where(np.abs(hi) * rstd > 1, hi, np.float32(0))
+    colsum = w.astype(np.float64).sum(1).astype(np.float32)
+    acc = (h - c[:, None]) @ w.T
+    rest = (hi - c) + lo
+    return rstd[:, None] * (acc - rest[:, None] * colsum[None, :])
+
+
+@pytest.mark.parametrize("offset", [0.0, 0.9, 1.1, 10.0, 100.0])
+def test_folded_layernorm_bar_separates_the_folds(offset):
+    """The bar of the device test of the folded LayerNorm (1e-5 against LayerNorm then
+    matmul_nt) passes the GEMM's per-row rule at every offset, including rows on either
+    side of its one-sigma threshold, and fails the fold that subtracts mean * colsum after
+    the product once rows sit 100 sigma from zero: the test tells them apart."""
+    rng = np.random.default_rng(3)
+    h = (offset + rng.standard_normal((64, 768))).astype(np.float32)
+    w = (0.02 * rng.standard_normal((256, 768))).astype(np.float32)
+    want = oracle.matmul_nt(oracle.layer_norm(h, np.ones(768, np.float32), None, np.float32(1e-12)), w,
+                            threads=8)
+    for mode in ("rows", "centre"):
+        err = np.abs(_folded_layernorm_f32(h, w, mode) - want).max()
+        assert err <= 1e-5, (mode, err)
+    after = np.abs(_folded_layernorm_f32(h, w, "after") - want).max()
+    if offset >= 100:
+        assert after > 1e-5, after
+    elif offset <= 1.1:
+        assert after <= 5e-6, after  # within the threshold the mean may come out afterwards
