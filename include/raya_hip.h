@@ -86,7 +86,7 @@ const char *raya_build_info(void);
 
 /* AttentionKernel::attend (crates/raya-kernels/src/attention.rs:113-125) on
  * host slices: validates like validate() (attention.rs:128-170) plus the
- * HIP kernel's limits (head_dim <= 128), copies q/k/v to the current device,
+ * HIP kernel's limits (head_dim <= 256), copies q/k/v to the current device,
  * runs the fused kernel, copies out back and synchronises.  out is fully
  * overwritten; rows >= valid_len are exact zeros. */
 int raya_attend(const raya_attn_shape *shape, const raya_attn_params *params,

@@ -1190,6 +1190,17 @@ hipError_t launch_attention(const AttnLaunch &a, hipStream_t stream) {
     case 96: return launch_dp<96>(a, stream);
     case 112: return launch_dp<112>(a, stream);
     case 128: return launch_dp<128>(a, stream);
+    // Above 128 the contraction is padded to the next of four widths (at most 1/8 of it
+    // zeros from 144 up): K/V tiles of 64 keys take 2 x 64 x DP floats of LDS (128 KB at
+    // 256, one workgroup per compute unit).
+    case 144:
+    case 160: return launch_dp<160>(a, stream);
+    case 176:
+    case 192: return launch_dp<192>(a, stream);
+    case 208:
+    case 224: return launch_dp<224>(a, stream);
+    case 240:
+    case 256: return launch_dp<256>(a, stream);
     default: return hipErrorInvalidValue;
     }
 }

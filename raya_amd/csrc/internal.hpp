@@ -33,7 +33,7 @@ struct AttnLaunch {
 };
 
 // Largest head_dim the fused attention kernel is instantiated for.
-constexpr int kMaxHeadDim = 128;
+constexpr int kMaxHeadDim = 256;
 
 hipError_t launch_attention(const AttnLaunch &a, hipStream_t stream);
 

@@ -92,9 +92,11 @@ def test_matches_naive_at_edge_lengths(hip_attention, name):
         assert (got[:, valid:, :] == 0).all()
 
 
-@pytest.mark.parametrize("d", [8, 16, 24, 40, 64, 72, 96, 128])
+@pytest.mark.parametrize("d", [8, 16, 24, 40, 64, 72, 96, 128, 136, 152, 192, 200, 256])
 def test_matches_naive_for_every_head_dim(hip_attention, d):
-    """equivalence.rs:77-112 and dispatch.rs head dims (8..128)."""
+    """equivalence.rs:77-112 and dispatch.rs head dims (8..128), and the widths validate()
+    accepts past 128 (simd_kernels.rs:15, :42 test the micro-kernels at 136): 136 and 152 on
+    the 160-wide instantiation, 192, 200 (224-wide) and 256."""
     for name in ("block3", "window64", "block_diag64"):
         mask, okind, block, window = MASKS[name]
         for seq, valid in ((300, 300), (200, 130)):
@@ -454,14 +456,14 @@ def test_full_size_block3_b32_l2048_against_float64(hip_attention):
 
 def test_random_sweep_against_the_oracle(hip_attention):
     """48 random batched launches against the oracle: batch 1-4, heads 1-3, seq 1-700,
-    every head_dim multiple of 8 up to 128, every mask with random widths (BlockDiag(b) and
+    every head_dim multiple of 8 up to 256, every mask with random widths (BlockDiag(b) and
     Sliding(w) from 1 to past seq), valid lengths anywhere in [0, seq] (out-of-range values
     are clamped by the entry point), and negative or enlarged scales."""
     rng = np.random.default_rng(2024)
     kinds = ["block3", "window64", "full", "sliding", "block_diag"]
     for case in range(48):
         b, h = int(rng.integers(1, 5)), int(rng.integers(1, 4))
-        s, d = int(rng.integers(1, 701)), 8 * int(rng.integers(1, 17))
+        s, d = int(rng.integers(1, 701)), 8 * int(rng.integers(1, 33))
         kind = kinds[case % len(kinds)]
         arg = int(rng.integers(1, s + 80))
         if kind == "sliding":

@@ -67,11 +67,12 @@ def test_bad_arguments_are_errors_not_panics():
 
 
 def test_hip_limits_are_unsupported_not_wrong():
+    """head_dim 264 is past the widest instantiation (256): Unsupported, before any device work."""
     k = R.HipAttention()
-    shape = R.AttnShape(1, 2, 136)
+    shape = R.AttnShape(1, 2, 264)
     buf = _ok(shape)
     with pytest.raises(R.UnsupportedError):
-        k.attend(shape, R.AttnParams.new(R.Mask.WINDOW64, 2, 136), buf, buf, buf, _ok(shape))
+        k.attend(shape, R.AttnParams.new(R.Mask.WINDOW64, 2, 264), buf, buf, buf, _ok(shape))
     with pytest.raises(R.ShapeError):
         k.attend(R.AttnShape(1, 4, 8), R.AttnParams.new(R.Mask.block_diag(0), 4, 8),
                  *(_ok(R.AttnShape(1, 4, 8)) for _ in range(4)))
@@ -170,14 +171,14 @@ def test_header_builds_a_plain_c_client(tmp_path):
 
 def test_length_before_hip_limits():
     """validate() checks the buffer lengths right after the block (attention.rs:159-168),
-    before anything the HIP kernel adds: head_dim 136 (past the kernel's 128) with a short
+    before anything the HIP kernel adds: head_dim 264 (past the kernel's 256) with a short
     `q` is a Length error, as the reference gives."""
     k = R.HipAttention()
-    shape = R.AttnShape(1, 2, 136)
+    shape = R.AttnShape(1, 2, 264)
     buf = _ok(shape)
     with pytest.raises(R.LengthError) as e:
-        k.attend(shape, R.AttnParams.new(R.Mask.WINDOW64, 2, 136), buf[:5], buf, buf, _ok(shape))
-    assert (e.value.name, e.value.got, e.value.expected) == ("q", 5, 272)
+        k.attend(shape, R.AttnParams.new(R.Mask.WINDOW64, 2, 264), buf[:5], buf, buf, _ok(shape))
+    assert (e.value.name, e.value.got, e.value.expected) == ("q", 5, 528)
     # the mask extension's own check also comes after the lengths
     s8 = R.AttnShape(1, 4, 8)
     with pytest.raises(R.LengthError):
