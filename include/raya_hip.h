@@ -122,12 +122,13 @@ int raya_attend_with_stages(const raya_attn_shape *shape, const raya_attn_params
  * slots of RAYA_STATIC_ATTEND_MAX_NUMEL floats (64 MiB on every device the
  * library runs on, held until the process ends) instead of raya_attend's
  * grow-only workspace, and the copies and the launch run on `stream` (a
- * hipStream_t; NULL is the null stream), which is synchronised before the call
- * returns.  Same checks and errors as raya_attend, then RAYA_ERR_UNSUPPORTED
- * when heads * seq * head_dim exceeds RAYA_STATIC_ATTEND_MAX_NUMEL.  The array
- * is shared by every call in the process; calls are serialised on one lock, so
- * they never overlap on a device.  Nothing in it needs clearing: each call
- * overwrites the q, k, v and out slots it uses. */
+ * hipStream_t of the current device; NULL is the null stream), which is
+ * synchronised before the call returns.  Same checks and errors as raya_attend,
+ * then RAYA_ERR_UNSUPPORTED when heads * seq * head_dim exceeds
+ * RAYA_STATIC_ATTEND_MAX_NUMEL or the stream belongs to another device.  Each
+ * device's array is shared by every call on that device; those calls are
+ * serialised on a per-device lock, so they never overlap.  Nothing in it needs
+ * clearing: each call overwrites the q, k, v and out slots it uses. */
 #define RAYA_STATIC_ATTEND_MAX_NUMEL 4194304
 int raya_attend_static(const raya_attn_shape *shape, const raya_attn_params *params, const float *q,
                        size_t q_len, const float *k, size_t k_len, const float *v, size_t v_len, float *out,

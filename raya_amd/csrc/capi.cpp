@@ -137,17 +137,41 @@ bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 constexpr size_t kStaticSlotFloats = RAYA_STATIC_ATTEND_MAX_NUMEL;
 static __device__ __align__(256) float scratch[4 * kStaticSlotFloats];
 
-std::mutex g_static_mutex;  // held for a whole call: calls on any device run one at a time
+// One lock per device, held for a whole call: calls on one device run one at a time, calls on
+// different devices (each with its own copy of the array) do not wait for each other.
+constexpr int kMaxStaticDevices = 64;
+std::mutex g_static_mutex[kMaxStaticDevices];
+std::mutex g_static_ptr_mutex;  // guards g_static_ptr
 std::unordered_map<int, float *> g_static_ptr;
 
-int static_scratch(float **ptr) {
+// The current device, checked against the stream's (a stream of another device would stage
+// into this device's array from that device's queue).
+int static_device(hipStream_t stream, int *out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail_device(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxStaticDevices)
+        return fail(RAYA_ERR_UNSUPPORTED, "unsupported: device %d is past the static array's %d devices", dev,
+                    kMaxStaticDevices);
+    if (stream) {
+        hipDevice_t sdev = 0;
+        e = hipStreamGetDevice(stream, &sdev);
+        if (e != hipSuccess) return fail_device(e, "hipStreamGetDevice");
+        if ((int)sdev != dev)
+            return fail(RAYA_ERR_UNSUPPORTED, "unsupported: the stream belongs to device %d, the current device is %d",
+                        (int)sdev, dev);
+    }
+    *out = dev;
+    return RAYA_OK;
+}
+
+// The array's address on device `dev` (current), looked up once per device.
+int static_scratch(int dev, float **ptr) {
+    std::lock_guard<std::mutex> lock(g_static_ptr_mutex);
     auto it = g_static_ptr.find(dev);
     if (it == g_static_ptr.end()) {
         void *p = nullptr;
-        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || p == nullptr) return fail_device(e, "hipGetSymbolAddress(scratch)");
         it = g_static_ptr.emplace(dev, (float *)p).first;
     }
@@ -192,14 +216,16 @@ static int attend_host(const raya_attn_shape *shape, const raya_attn_params *par
     if (numel == 0) return ok();
     if (!q || !k || !v || !out) return fail(RAYA_ERR_SHAPE, "invalid shape: null buffer");
 
-    std::lock_guard<std::mutex> lock(fixed ? g_static_mutex : g_ws_mutex);
+    int static_dev = 0;
+    if (fixed && (rc = static_device((hipStream_t)user_stream, &static_dev))) return rc;
+    std::lock_guard<std::mutex> lock(fixed ? g_static_mutex[static_dev] : g_ws_mutex);
     void *base = nullptr;
     hipStream_t stream = nullptr;
     const size_t bytes = numel * sizeof(float);
     size_t slot = (bytes + 255) / 256 * 256;
     if (fixed) {
         float *sp = nullptr;
-        rc = static_scratch(&sp);
+        rc = static_scratch(static_dev, &sp);
         if (rc) return rc;
         base = sp;
         slot = kStaticSlotFloats * sizeof(float);

@@ -51,7 +51,10 @@ class PostLNLayer:
             self.w[name] = t
         self.heads, self.eps = heads, eps
         self.mask = mask if mask is not None else Mask.block_diag(64)
-        self._ws = None
+        # One workspace per stream, allocated on that stream: the caching allocator then
+        # orders its reuse, after a growth frees it, behind the launches on that stream, and
+        # forwards on different streams never share the qkv / context / sum buffers.
+        self._ws = {}
 
     def _desc(self, batch: int, seq: int):
         desc = C.PostLNLayerC(batch, seq, self.hidden, self.heads, self.ffn, self.mask.kind, 0, self.mask.arg,
@@ -76,6 +79,8 @@ class PostLNLayer:
         if not isinstance(valid_len, torch.Tensor) or valid_len.dtype != torch.int32 \
                 or valid_len.numel() != b or not valid_len.is_cuda:
             raise ShapeError("invalid shape: valid_len must be a GPU int32 tensor of batch entries")
+        if valid_len.device != dev:
+            raise TypeError(f"valid_len is on {valid_len.device}, the layer's weights on {dev}")
         if out is None:
             out = torch.empty_like(x)
         elif out.shape != x.shape or out.dtype != torch.float32 or not out.is_contiguous():
@@ -84,11 +89,15 @@ class PostLNLayer:
         need = C.lib().raya_postln_workspace_bytes(ctypes.byref(desc))
         if need == 0:
             _raise_last(C.last_error().code)
-        if self._ws is None or self._ws.numel() * 4 < need:
-            self._ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=x.device)
+        st = stream if stream is not None else torch.cuda.current_stream(dev)
+        ws = self._ws.get(st.cuda_stream)
+        if ws is None or ws.numel() * 4 < need:
+            with torch.cuda.stream(st):
+                ws = torch.empty((need + 3) // 4, dtype=torch.float32, device=dev)
+            self._ws[st.cuda_stream] = ws
         rc = C.lib().raya_postln_layer_forward(ctypes.byref(desc), _dev_ptr(valid_len, "valid_len"), _dev_ptr(x, "x"),
-                                               _dev_ptr(out, "out"), _dev_ptr(self._ws, "workspace"), need,
-                                               _stream_ptr(stream))
+                                               _dev_ptr(out, "out"), _dev_ptr(ws, "workspace"), need,
+                                               _stream_ptr(st))
         if rc:
             _raise_last(rc)
         return out

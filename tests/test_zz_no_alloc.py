@@ -4,7 +4,9 @@ with its device staging in the library's static array instead of allocated memor
 CPU: the size limit and the reference's errors come back before any GPU work.
 GPU: two calls in a row, the second on a smaller input, each equal to raya_attend's output bit
 for bit and within the oracle's bar (max-abs and rel-L2 1e-5 against Naive); the device's free
-memory does not move across the calls."""
+memory does not move across the two calls (a warm-up call first loads the code object that holds
+the static array).  The calls run on a stream of the current device, which the entry point
+checks."""
 import ctypes
 
 import numpy as np
@@ -56,12 +58,18 @@ CASES = [
 
 @pytest.mark.gpu
 def test_two_calls_match_raya_attend_without_allocating():
-    """The reference outputs come first (raya_attend grows its own workspace), then two static
-    calls in a row.  The first static call may load the code object that holds the static
-    array; across the second the device's free memory stays put."""
+    """The reference outputs come first (raya_attend grows its own workspace), then a warm-up
+    static call on a tiny input (it may load the code object that holds the static array), then
+    the two static calls under test; across both the device's free memory stays put."""
     import torch
 
     assert torch.cuda.is_available(), "needs a GPU"
+    stream = torch.cuda.Stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    tiny = np.ones(8, np.float32)
+    rc = call_static(R.AttnShape(1, 1, 8), R.AttnParams.new(R.Mask.BLOCK3, 1, 8), tiny, tiny, tiny,
+                     np.zeros(8, np.float32), sp)
+    assert rc == C.RAYA_OK, C.last_error().message.decode()
     kernel = R.HipAttention()
     inputs, wants = [], []
     for h, s, d, mask, kind, block, window, valid, seed in CASES:
@@ -72,11 +80,11 @@ def test_two_calls_match_raya_attend_without_allocating():
         inputs.append((q, k, v, shape, params))
         wants.append(want)
     torch.cuda.synchronize()
-    free = []
+    free = [torch.cuda.mem_get_info()[0]]
     for (h, s, d, mask, kind, block, window, valid, seed), (q, k, v, shape, params), want in zip(CASES, inputs, wants):
         print(f"static attend: H={h} L={s} D={d} {mask.name()} valid {valid}", flush=True)
         got = np.full(q.size, np.nan, np.float32)
-        rc = call_static(shape, params, q.ravel(), k.ravel(), v.ravel(), got)
+        rc = call_static(shape, params, q.ravel(), k.ravel(), v.ravel(), got, sp)
         assert rc == C.RAYA_OK, C.last_error().message.decode()
         free.append(torch.cuda.mem_get_info()[0])
         assert np.array_equal(got, want)
@@ -85,4 +93,4 @@ def test_two_calls_match_raya_attend_without_allocating():
         rel = np.sqrt((diff ** 2).sum() / (naive.astype(np.float64) ** 2).sum())
         assert diff.max() < 1e-5 and rel < 1e-5, (diff.max(), rel)
         assert (got.reshape(q.shape)[:, valid:] == 0).all()
-    assert free[1] >= free[0] - (2 << 20), free
+    assert min(free[1:]) >= free[0] - (2 << 20), free
