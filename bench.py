@@ -82,7 +82,11 @@ GRAPH_BELOW_MS = 0.05
 # Ordered so that lines drawing the same inputs (same batch, another mask) follow each other.
 SUBLINES = ["attn_b32_h12_l2048_d64_block3",
             "attn_b1_h12_l512_d64_blockdiag64", "attn_b1_h12_l512_d64_block3",
-            "attn_b4_h12_l16384_d64_blockdiag128", "attn_b4_h12_l16384_d64_block3"]
+            "attn_b4_h12_l16384_d64_blockdiag128", "attn_b4_h12_l16384_d64_block3",
+            "refbench_h16_l8192_d64_window64"]
+# The trait's own path (host slices in and out, AttentionKernel::attend): the one-sequence
+# workloads and the reference bench's smallest shape.
+HOST_SLICE = ["attn_b1_h12_l512_d64_blockdiag64", "attn_b1_h12_l512_d64_block3", "refbench_h16_l2048_d64_block3"]
 _INPUTS: dict = {}
 
 
@@ -846,6 +850,119 @@ def predict_bench(tokens: list[int], repeats: int, warmup: int, cap_s: float) ->
     }
 
 
+def bench_host_slice(calls: int, warmup: int) -> dict:
+    """raya_attend through HipAttention.attend on host (numpy) slices, as a Network holding
+    the kernel would call it per layer (crates/raya-kernels/benches/local_attention.rs:102,
+    :125 time the trait the same way): each call copies q, k, v to the device, launches and
+    copies out back, then synchronises.  Median and p90 over `calls` calls, and the same
+    launch on device-resident inputs (graph replays) beside it."""
+    import numpy as np
+
+    import raya_amd as R
+
+    kernel = R.HipAttention()
+    res = {}
+    for name in HOST_SLICE:
+        wl = WORKLOADS[name]
+        (q, k, v), valid = attention_inputs(wl)
+        h, s_, d = wl["heads"], wl["seq"], wl["head_dim"]
+        q, k, v = (np.ascontiguousarray(x[0]).ravel() for x in (q, k, v))
+        out = np.empty_like(q)
+        shape = R.AttnShape(h, s_, d)
+        params = R.AttnParams.new(kernel_mask(wl["mask"]), int(valid[0]), d)
+        log(f"host-slice attend {name}: {calls} calls")
+        for _ in range(warmup):
+            kernel.attend(shape, params, q, k, v, out)
+        t = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            kernel.attend(shape, params, q, k, v, out)
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        moved = 4 * 4 * q.size  # q, k, v to the device, out back
+        res[name] = {"p50_ms": statistics.median(t) * 1e3, "p90_ms": t[(9 * len(t)) // 10] * 1e3,
+                     "calls": calls, "bytes_moved": moved,
+                     "host_link_gbs": moved / statistics.median(t) / 1e9}
+    return res
+
+
+def _r(x, digits: int = 4):
+    """x rounded to `digits` significant digits (floats only)."""
+    if isinstance(x, float):
+        return float(f"{x:.{digits}g}")
+    return x
+
+
+def compact(result: dict) -> dict:
+    """The line printed to stdout: the contract's keys, the headline's figures, and a `lines`
+    map (one short entry per measured workload) last, small enough that a reader keeping the
+    tail of stdout sees all of it.  The full document goes to --detail-out."""
+    keep = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+            "scaling", "vs_baseline", "dtype", "data")
+    out = {k: _r(result[k]) if k in ("value", "ms_per_step") else result[k] for k in keep}
+    c = result["config"]
+    out["config"] = {k: c[k] for k in ("workload", "batch", "heads", "seq", "head_dim", "mask", "valid_len",
+                                       "flop_per_step", "bytes_per_step")}
+    out["kernel_ms"] = _r(result["kernel_ms"])
+    if "per_launch_ms" in result:
+        out["per_launch_median_ms"] = _r(result["per_launch_ms"]["median"])
+    out["kernel_tflops"] = _r(result["kernel_tflops"])
+    out["mfma_frac"] = _r(result["mfma_frac"])
+    rf = result["roofline"]
+    out["roofline"] = {k: _r(rf[k]) for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")}
+    if "cpu_baseline" in result:
+        cb = result["cpu_baseline"]
+        out["cpu_baseline"] = {k: _r(cb[k]) for k in ("value", "unit", "cores", "kind", "sample", "t1_value",
+                                                      "gpu_vs_cpu_max_abs") if k in cb}
+    if "stage_split" in result:
+        ss = result["stage_split"]
+        out["stage_split_pct"] = {k.replace("_pct", "").replace("_of_wave_cycles", ""): _r(v, 3)
+                                  for k, v in ss.items() if k.endswith("pct")}
+    m = result.get("meta", {})
+    out["meta"] = {"label": m.get("label"), "commit": str(m.get("git_commit", ""))[:12],
+                   "cpu": m.get("cpu_model"), "threads": m.get("threads")}
+
+    lines = {}
+    for name, ln in result.get("workloads", {}).items():
+        e = {"kernel_ms": _r(ln["kernel_ms"]), "tflops": _r(ln["kernel_tflops"]),
+             "bound": ln["roofline"]["bound"], "frac": _r(ln["roofline"]["frac"], 3)}
+        if "cpu_baseline" in ln:
+            e["cpu_tflops"] = _r(ln["cpu_baseline"]["value"])
+            e["max_abs"] = _r(ln["cpu_baseline"]["gpu_vs_cpu_max_abs"], 2)
+            if "naive_t1_value" in ln["cpu_baseline"]:
+                e["cpu_naive_t1_tflops"] = _r(ln["cpu_baseline"]["naive_t1_value"])
+        lines[name] = e
+    enc = result.get("encoder")
+    if enc:
+        e = {"seq_per_s": _r(enc["sequences_per_s"]), "tflops": _r(enc["tflops"]),
+             "mfma_frac": _r(enc["mfma_frac"], 3)}
+        if "cpu_baseline" in enc:
+            e["cpu_seq_per_s"] = _r(enc["cpu_baseline"]["value"])
+            e["act_logits_max_abs"] = _r(enc["cpu_baseline"]["gpu_vs_cpu_act_logits_max_abs"], 2)
+        lines[enc["workload"]] = e
+        for r in enc.get("predict_latency", []):
+            lines[f"predict_l{r['tokens']}"] = {"p50_ms": _r(r["p50_ms"]), "p90_ms": _r(r["p90_ms"])}
+    lay = result.get("encoder_layer")
+    if lay:
+        lines[lay["workload"]] = {"seq_per_s": _r(lay["sequences_per_s"]), "tflops": _r(lay["tflops"]),
+                                  "mfma_frac": _r(lay["mfma_frac"], 3)}
+    pl = result.get("postln_layer")
+    if pl:
+        e = {"seq_per_s": _r(pl["sequences_per_s"]), "tflops": _r(pl["tflops"]), "mfma_frac": _r(pl["mfma_frac"], 3)}
+        if "cpu_baseline" in pl:
+            e["cpu_seq_per_s"] = _r(pl["cpu_baseline"]["value"])
+            e["max_abs"] = _r(pl["cpu_baseline"]["gpu_vs_cpu_max_abs"], 2)
+        lines[pl["workload"]] = e
+    gm = result.get("encoder_gemms")
+    if gm:
+        for shp, v in gm.get("plain_vs_torch_mm", {}).items():
+            lines[f"gemm_{shp}"] = {"tflops": _r(v["tflops"]), "torch_mm_tflops": _r(v["torch_mm_tflops"])}
+    for name, v in result.get("host_slice_attend", {}).items():
+        lines[f"host_slice_{name}"] = {"p50_ms": _r(v["p50_ms"]), "p90_ms": _r(v["p90_ms"])}
+    out["lines"] = lines
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -871,6 +988,8 @@ def main() -> int:
     ap.add_argument("--predict-repeats", type=int, default=20)
     ap.add_argument("--predict-warmup", type=int, default=3)
     ap.add_argument("--predict-cap-s", type=float, default=60.0)
+    ap.add_argument("--detail-out", default=None,
+                    help="also write the full bench document (every field of every leg) to this path")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus})",
@@ -966,7 +1085,12 @@ def main() -> int:
         result["encoder_gemms"] = bench_gemms(20, 3)
         result["postln_layer"] = bench_postln(args.encoder_steps, args.encoder_warmup, min(args.cpu_seconds, 3.0),
                                               cpu=not args.no_cpu_baseline)
-    print(json.dumps(result), flush=True)
+    if args.workload == DEFAULT and not args.no_sublines:
+        result["host_slice_attend"] = bench_host_slice(50, 5)
+    if args.detail_out:
+        with open(args.detail_out, "w") as f:
+            json.dump(result, f, indent=1)
+    print(json.dumps(compact(result)), flush=True)
     return 0
 
 
