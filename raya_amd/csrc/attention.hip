@@ -584,8 +584,12 @@ __device__ __forceinline__ void lap(StageClock *c, uint64_t &bucket) {
 // before the combine.
 // MK >= 0: the mask kind is fixed at compile time; SINGLE: every item's keys fit one
 // tile (BlockDiag(b) with b dividing 64).  Both only drop code the launch has ruled out.
+//
+// MAXT > 0 (the direct path, items of at most MAXT tiles): every tile's K/V subtile
+// is loaded into registers before the first is computed, so the tile loads' latencies
+// overlap each other rather than each one the previous tile's arithmetic.
 template <int DP, bool FUSED, bool TIMED, bool SKIP = false, bool SPLIT = false, int MK = -1,
-          bool SINGLE = false>  // head_dim padded to a multiple of 16
+          bool SINGLE = false, int MAXT = 0>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs, StageClock *clk) {
     static_assert(!FUSED || DP == 64, "the fused issue is written for head_dim 64");
@@ -598,6 +602,9 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     // go straight into registers (no LDS staging, no barrier before the combine), the
     // next tile's loaded while the current one is computed.
     constexpr bool DIRECT = SPLIT && FUSED;
+    constexpr bool ALL = MAXT > 0;
+    static_assert(!ALL || (DIRECT && !TIMED), "whole-item prefetch is a variant of the direct path");
+    constexpr int kUnroll = ALL ? MAXT : 1;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -747,6 +754,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         }
     };
     float4 kcur[4], vcur[4];
+    float4 kall[kUnroll][4], vall[kUnroll][4];
     if constexpr (DIRECT) {
         const float *qp = a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)min(qi, valid - 1) * a.q_rs + 4 * g;
 #pragma unroll
@@ -757,7 +765,14 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             qreg[4 * c + 2] = x.z;
             qreg[4 * c + 3] = x.w;
         }
-        load_sub(kt0, kcur, vcur);
+        if constexpr (ALL) {
+            // Steps past the item's last tile load that tile again (never computed).
+#pragma unroll
+            for (int j = 0; j < kUnroll; ++j) load_sub(tile_at(min(j, n_tiles - 1)), kall[j], vall[j]);
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            load_sub(kt0, kcur, vcur);
+        }
         // A single tile's loads all leave here: the scheduler would otherwise sink each
         // one next to its first use and wait for it alone.
         if constexpr (SINGLE) __builtin_amdgcn_sched_barrier(0);
@@ -797,12 +812,21 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     float l = 0.f;        // this lane's partial sum of weights
 
     if constexpr (TIMED) clk->last = clock_now();
-    for (int j = 0; j < n_tiles; ++j) {
+    // The whole-item prefetch runs its steps to MAXT, fully unrolled (its register
+    // sets are indexed by the step); the steps past the item's tiles idle.
+#pragma unroll kUnroll
+    for (int j = 0; j < (ALL ? kUnroll : n_tiles); ++j) {
         const int kt = tile_at(j);
         int kx, ky;
         step_keys(kt, kx, ky);
         float4 knext[4], vnext[4];
-        if constexpr (DIRECT) {
+        if constexpr (ALL) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                kcur[c] = kall[j][c];
+                vcur[c] = vall[j][c];
+            }
+        } else if constexpr (DIRECT) {
             if (j + 1 < n_tiles) load_sub(tile_at(j + 1), knext, vnext);
         }
         if (!DIRECT && j != 0) {
@@ -831,7 +855,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 for (int e = 0; e < 4; ++e) qreg[4 * c + e] = in ? qreg[4 * c + e] * q_sign : 0.f;
             }
         }
-        bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
+        bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo && (!ALL || j < n_tiles);
         // Sliding windows: the 16-key subtiles outside the union of the wave's
         // key intervals [w_first.lo, w_last.hi) hold no live key for any of its
         // rows (about a quarter of an item's subtiles at Window64); such a tile
@@ -912,7 +936,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 lap(clk, clk->pv);
             }
         }
-        if constexpr (DIRECT) {
+        if constexpr (DIRECT && !ALL) {
             if (j + 1 < n_tiles) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -1068,6 +1092,17 @@ __global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>)) atte
     attend_body<DP, FUSED, false, false, true, MK, SINGLE>(a, p, ks, vs, nullptr);
 }
 
+// The split kernel at head_dim 64 for items of at most MAXT tiles, every tile's K/V
+// loads issued before the first tile is computed.  2 waves per SIMD hold the MAXT
+// register sets (239 VGPRs at MAXT = 6); the small grids this kernel serves place at
+// most two workgroups per compute unit.
+template <int MAXT>
+__global__ void __launch_bounds__(kThreads, 2) attend_split_all_kernel(const AttnLaunch a, const Plan p) {
+    __shared__ __attribute__((aligned(16))) float ks[kKeys * 64];
+    __shared__ __attribute__((aligned(16))) float vs[kKeys * 64];
+    attend_body<64, true, false, false, true, -1, false, MAXT>(a, p, ks, vs, nullptr);
+}
+
 // The same kernel with the stage clock.  Per-wave totals are summed in LDS,
 // then one thread per stage adds the workgroup's sum to the caller's totals.
 // An item whose rows are all padding returns from the body in every wave with
@@ -1122,6 +1157,31 @@ bool use_split(const AttnLaunch &a) {
     return items < kSplitBelow;
 }
 
+// The most 64-key tiles one 16-row item's key interval spans (every row valid; a
+// shorter valid length only clips intervals).
+int64_t max_item_tiles(const AttnLaunch &a) {
+    const int64_t b = a.mask_arg;
+    int64_t span;
+    switch (a.mask_kind) {
+    case RAYA_MASK_BLOCK3: span = 3 * RAYA_BLOCK; break;  // the rows share one 128-block
+    case RAYA_MASK_WINDOW64: span = kSplitRows + 2 * RAYA_WINDOW; break;
+    case RAYA_MASK_FULL: span = a.seq; break;
+    case RAYA_MASK_SLIDING: span = kSplitRows + 2 * b; break;
+    default:  // BlockDiag(b): one block when 16 divides b, else the blocks 16 rows touch
+        span = b % kSplitRows == 0 ? b : b * ((kSplitRows - 1) / b + 2);
+        break;
+    }
+    span = std::min<int64_t>(span, a.seq);
+    return (span + kKeys - 1) / kKeys;
+}
+
+// RAYA_ATTN_PREFETCH=0 keeps the one-tile-ahead loads of the split kernel on items of
+// up to six tiles.
+bool prefetch_all() {
+    const char *e = std::getenv("RAYA_ATTN_PREFETCH");
+    return !(e && !std::strcmp(e, "0"));
+}
+
 template <int DP, bool FUSED = false>
 hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const bool split = use_split(a);
@@ -1146,6 +1206,18 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
             hipLaunchKernelGGL((attend_timed_kernel<DP, FUSED, false, true>), grid, block, 0, stream, a, p);
         else if (FUSED && a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
             hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, RAYA_MASK_BLOCKDIAG, true>), grid, block, 0, stream, a, p);
+        else if (FUSED && prefetch_all() && max_item_tiles(a) >= 2 && max_item_tiles(a) <= 6) {
+            // (Single-tile items have no later load to overlap.)
+            const int64_t t = max_item_tiles(a);
+            if (t <= 2)
+                hipLaunchKernelGGL((attend_split_all_kernel<2>), grid, block, 0, stream, a, p);
+            else if (t <= 3)
+                hipLaunchKernelGGL((attend_split_all_kernel<3>), grid, block, 0, stream, a, p);
+            else if (t <= 4)
+                hipLaunchKernelGGL((attend_split_all_kernel<4>), grid, block, 0, stream, a, p);
+            else
+                hipLaunchKernelGGL((attend_split_all_kernel<6>), grid, block, 0, stream, a, p);
+        }
         else
             hipLaunchKernelGGL((attend_split_kernel<DP, FUSED>), grid, block, 0, stream, a, p);
         return hipGetLastError();

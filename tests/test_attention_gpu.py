@@ -20,12 +20,17 @@ from tests.conftest import GOLDEN
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True, params=["64", "16"], ids=["items64", "items16"])
+@pytest.fixture(autouse=True, params=["64", "16", "16p0"], ids=["items64", "items16", "items16_tile_ahead"])
 def item_rows(request, monkeypatch):
     """Every test runs on both attention kernels: 64-row items (the large grids) and
-    16-row items with each tile's keys split over the waves (the small grids)."""
-    monkeypatch.setenv("RAYA_ATTN_ITEMS", request.param)
-    return int(request.param)
+    16-row items with each tile's keys split over the waves (the small grids).  At
+    head_dim 64 the latter loads all of an item's tiles up front when they are at most
+    six, and one tile ahead otherwise, or everywhere with RAYA_ATTN_PREFETCH=0."""
+    rows, _, prefetch = request.param.partition("p")
+    monkeypatch.setenv("RAYA_ATTN_ITEMS", rows)
+    if prefetch:
+        monkeypatch.setenv("RAYA_ATTN_PREFETCH", prefetch)
+    return int(rows)
 
 MAX_ABS = 1e-5
 REL_L2 = 1e-5
