@@ -280,11 +280,11 @@ __device__ __forceinline__ float row16_sum(float x) {
 }
 
 // Epilogue through LDS, for out (and residual) with row strides a multiple of 4
-// floats and 16-byte aligned bases.  Bias, activation, GeGLU and RoPE are
-// applied in the accumulator layout, as in epilogue(); each wave then writes
-// its y rows to its own LDS area and reads them back row-major, so that the
-// residual reads and the stores are float4 with 256-byte (GeGLU: 128-byte) row
-// segments: a quarter of the store instructions of the accumulator layout.
+// floats and 16-byte aligned bases.  Bias, activation and GeGLU are applied in the
+// accumulator layout, as in epilogue(); each wave then writes its y rows to its own
+// LDS area and reads them back row-major, so that RoPE reads its tables as float4,
+// and the residual reads and the stores are float4 with 256-byte (GeGLU: 128-byte)
+// row segments: a quarter of the store instructions of the accumulator layout.
 // Staged row strides: lanes i and i + 32 of a write are 4 rows apart, and
 // 4 * stride = 32 (mod 64) puts them on disjoint banks.
 constexpr int kStageStride = 72;      // 64 columns per wave
@@ -304,6 +304,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&
                                                 int wm, int wn, int li, int h, int lane, float *stg,
                                                 const float2 *rownorm, const float (&cs)[2]) {
     constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
+    static_assert(!(ROPE && STATS), "RoPE outputs carry no row statistics");
     constexpr int COLS = GEGLU ? 32 : 64;  // output columns of this wave
     constexpr int S = GEGLU ? kStageStrideGlu : kStageStride;
     constexpr int C4 = COLS / 4;           // float4 per staged row
@@ -343,24 +344,63 @@ __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&
                 float y[2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) y[j] = activate<ACT>(g.bias ? acc[i][j][r] + bias[j] : acc[i][j][r]);
-                if constexpr (ROPE) {
-                    // Columns c and c + 32 of one 64-wide head sit in the same lane
-                    // and register of acc[i][0] and acc[i][1].
-                    const int row = min(m0 + wm + 32 * i + rr, g.m - 1);
-                    if (c0 + li < g.rope_cols) {
-                        const int64_t t = (int64_t)g.positions[row] * (kRopeHeadDim / 2) + li;
-                        const float c = g.rope_cos[t], sn = g.rope_sin[t];
-                        const float x0 = y[0], x1 = y[1];
-                        y[0] = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
-                        y[1] = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, sn));
-                    }
-                }
                 stg[rr * S + li] = y[0];
                 stg[rr * S + 32 + li] = y[1];
             }
         }
         // LDS accesses of one wave complete in order: the reads below see the
         // writes above, and the next half's writes follow these reads.
+        if constexpr (ROPE && !GEGLU) {
+            // RoPE on row-major data: this wave's 64 columns are one head (n0 and wn are
+            // multiples of 64), so a lane takes the 16-byte chunks c4 and c4 + 8 of a row,
+            // columns c .. c + 3 and c + 32 .. c + 35 with c = 4 c4, and rotates each pair
+            // at frequencies c .. c + 3: one float4 of each table per 8 outputs.  Bias and
+            // activation came first, the residual comes after, as in epilogue().
+            const bool rot = c0 < g.rope_cols;  // the q and k sections: whole heads
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int idx = t * 64 + lane, rr = idx >> 3, c4 = idx & 7;
+                const int row = m0 + wm + 32 * i + rr;
+                if (row >= g.m) continue;
+                float4 x0 = *(const float4 *)&stg[rr * S + 4 * c4];
+                float4 x1 = *(const float4 *)&stg[rr * S + 32 + 4 * c4];
+                if (rot) {
+                    const int64_t tb = (int64_t)g.positions[row] * (kRopeHeadDim / 2) + 4 * c4;
+                    const float4 cs4 = *(const float4 *)(g.rope_cos + tb), sn4 = *(const float4 *)(g.rope_sin + tb);
+                    const auto turn = [](float &a, float &b, float c, float sn) {
+                        const float a0 = a, b0 = b;
+                        a = __fsub_rn(__fmul_rn(a0, c), __fmul_rn(b0, sn));
+                        b = __fadd_rn(__fmul_rn(b0, c), __fmul_rn(a0, sn));
+                    };
+                    turn(x0.x, x1.x, cs4.x, sn4.x);
+                    turn(x0.y, x1.y, cs4.y, sn4.y);
+                    turn(x0.z, x1.z, cs4.z, sn4.z);
+                    turn(x0.w, x1.w, cs4.w, sn4.w);
+                }
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int col = c0 + 32 * half + 4 * c4;
+                    if (col >= g.n) continue;
+                    float4 v = half ? x1 : x0;
+                    float *o = g.out + (int64_t)row * g.ldo + col;
+                    const float *res = g.residual ? g.residual + (int64_t)row * g.ldr + col : nullptr;
+                    if (col + 4 <= g.n) {
+                        if (res) {
+                            const float4 x = *(const float4 *)res;
+                            v.x += x.x;
+                            v.y += x.y;
+                            v.z += x.z;
+                            v.w += x.w;
+                        }
+                        *(float4 *)o = v;
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int q = 0; q < 4 && col + q < g.n; ++q) o[q] = res ? e[q] + res[q] : e[q];
+                    }
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int t = 0; t < 32 * C4 / 64; ++t) {
             const int idx = t * 64 + lane, rr = idx / C4, c4 = idx % C4;
