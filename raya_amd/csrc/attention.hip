@@ -975,7 +975,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             lsum += sw[w] * vs[(kWaves + w) * 64 + lane];
         }
         if (qi < (packed ? valid : a.seq)) {
-            const bool zero_row = !(qi < valid && lsum > 0.f);
+            const bool zero_row = qi >= valid || lsum == 0.f;
             const float inv = zero_row ? 0.f : 1.f / lsum;
             float *orow = ob + (int64_t)qi * a.o_rs + g * DQ;
             for (int c = wave; c < DQ / 4; c += kWaves) {
@@ -997,9 +997,10 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     }
 
     // Register r of oacc[n] holds dim g DQ + NT r + n of row qi.  Rows at or
-    // beyond valid, and rows with no weight, are stored as literal zeros: their
-    // accumulators are zero weights times V, which is NaN wherever V is not
-    // finite.
+    // beyond valid, and rows with no weight (an empty key range), are stored as
+    // literal zeros: their accumulators are zero weights times V, which is NaN
+    // wherever V is not finite.  A NaN weight sum (a NaN or +Inf score) makes the
+    // whole row NaN, as the reference's division by that sum does (naive.rs:53-61).
     if constexpr (FUSED) {
         // The wave's 16 x 64 output block goes through its quarter of the K tile
         // (no wave reads K after the last tile's V barrier) and leaves as whole
@@ -1010,7 +1011,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         // one chunk each) and the reads (one row, 16 chunks) touch 16
         // distinct chunk columns.
         float *st = ks + wave * 16 * 64;
-        const bool zero_row = !(qi < valid && l > 0.f);
+        const bool zero_row = qi >= valid || l == 0.f;
         const float inv = zero_row ? 0.f : 1.f / l;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -1034,7 +1035,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         return;
     }
     if (qi < (packed ? valid : a.seq)) {
-        const bool zero_row = !(qi < valid && l > 0.f);
+        const bool zero_row = qi >= valid || l == 0.f;
         const float inv = zero_row ? 0.f : 1.f / l;
         float *orow = ob + (int64_t)qi * a.o_rs + g * DQ;
 #pragma unroll

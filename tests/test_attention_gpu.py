@@ -546,6 +546,32 @@ def test_non_finite_v_outside_a_window(hip_attention):
         print(f"{mask.name()}: {int((~same).sum())} of {gc.size} rows outside the window are NaN in dim {c}")
 
 
+@pytest.mark.parametrize("name", ["block3", "window64", "full", "block_diag64", "sliding8"])
+def test_non_finite_scores_match_the_reference(hip_attention, name):
+    """NaN and Inf in Q and K against the restated Naive kernel (naive.rs:13-65): a NaN in one
+    query row makes that whole output row NaN (its weight sum is NaN); an +Inf key row makes
+    the rows that see it NaN (their maximum is +Inf, and Inf - Inf is NaN); a -Inf key row
+    weighs 0 and leaves them finite; a NaN key row makes the rows that see it NaN and leaves
+    the others untouched (masked keys score -Inf whatever Q.K gives).  NaN exactly where the
+    reference has NaN, every finite output within the bar, padded rows exact zeros."""
+    mask, okind, block, window = MASKS[name]
+    h, s, d, valid = 2, 320, 64, 301
+    q, k, v = oracle.qkv(h, s, d, 91)
+    qq = q.copy(); qq[:, 77, 2] = np.nan
+    kp = k.copy(); kp[0, 90, :] = np.inf; kp[1, 90, :] = -np.inf
+    kn = k.copy(); kn[:, 250, 5] = np.nan
+    for what, qx, kx in (("NaN in a query row", qq, k), ("Inf in a key row", q, kp), ("NaN in a key row", q, kn)):
+        got = run_hip(hip_attention, qx, kx, v, mask, valid, fill=7.0)
+        want = oracle_naive(qx, kx, v, okind, valid, block, window)
+        assert (got[:, valid:] == 0).all(), f"{what}: padded rows must be literal zeros"
+        assert np.isnan(want).any(), f"{what}: the case must reach the output"
+        assert np.array_equal(np.isnan(got), np.isnan(want)), \
+            f"{name}, {what}: NaN at {int(np.isnan(got).sum())} outputs, the reference at {int(np.isnan(want).sum())}"
+        fin = np.isfinite(want)
+        assert np.isfinite(got[fin]).all()
+        check_close(got[fin], want[fin], f"{name}, {what}")
+
+
 def test_scale_zero_weighs_allowed_keys_uniformly(hip_attention):
     """A zero scale makes every allowed key weigh the same (s = 0 for all, as the reference
     computes it); masked keys still weigh nothing."""
