@@ -136,12 +136,14 @@ def random_batch(rng, cfg, b, seq, k):
     return ids, valid, pos, mask, qtype
 
 
-@pytest.mark.parametrize("hidden,heads", [(128, 2), (64, 2), (256, 4), (96, 2)])
-def test_batch_matches_oracle_per_sequence(tmp_path, hidden, heads):
+@pytest.mark.parametrize("hidden,heads,inter", [(128, 2, None), (64, 2, None), (256, 4, None), (96, 2, None),
+                                                (128, 2, 200)])
+def test_batch_matches_oracle_per_sequence(tmp_path, hidden, heads, inter):
     """hidden 256: the row-in-registers LayerNorm (rows of a multiple of 256 floats); hidden 96:
     not a multiple of 64, so the LayerNorms stay kernels of their own (the others fold them
-    into the GEMMs)."""
-    cfg, cdir, w = make_model(tmp_path, hidden, heads)
+    into the GEMMs); intermediate size 200: not a multiple of 16, so the MLP's output GEMM
+    (depth 200) leaves the ring kernel and the norms stay unfolded."""
+    cfg, cdir, w = make_model(tmp_path, hidden, heads, inter=inter)
     model = M.Model.load(cdir)
     rng = np.random.default_rng(hidden)
     ids, valid, pos, mask, qtype = random_batch(rng, cfg, b=5, seq=200, k=4)
