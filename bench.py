@@ -294,6 +294,34 @@ def cpu_naive_t1(qkv, valid, wl) -> dict:
             "naive_t1_sample": f"whole workload, Naive restatement, 1 thread, {dt * 1e3:.1f} ms"}
 
 
+def f64_errors(qkv, valid, wl, got, cpu_out) -> dict:
+    """Distance of the GPU's and the CPU port's fp32 outputs from a float64 evaluation of the
+    same attention (torch on the host), on the first sequence, max-abs and RMS.  On the x20
+    outliers a score's fp32 rounding depends on the order its 64 products are summed in
+    (one chain of 64 fused steps on the matrix core, 16 chains of 4 in the AVX2 kernel), and
+    near-tied outlier scores turn that into max-abs differences of 1e-4 and more between any
+    two fp32 evaluations; the RMS says how close each is overall.  Block masks only
+    (BlockDiag(b) and Block3: each 128- or b-row query block against its key blocks)."""
+    import numpy as np
+    import torch
+
+    q, k, v = (torch.from_numpy(x[0].astype(np.float64)) for x in qkv)
+    vl = int(valid[0])
+    kind = wl["mask"][0]
+    blk = wl["mask"][1] if kind == "block_diag" else 128
+    exact = np.zeros((q.shape[0], vl, q.shape[2]), np.float64)
+    for q0 in range(0, vl, blk):
+        q1 = min(q0 + blk, vl)
+        lo, hi = (q0, q1) if kind == "block_diag" else (max(q0 - 128, 0), min(q0 + 256, vl))
+        s_ = torch.bmm(q[:, q0:q1], k[:, lo:hi].transpose(1, 2).contiguous()) * 0.125
+        exact[:, q0:q1] = torch.bmm(torch.softmax(s_, dim=-1), v[:, lo:hi]).numpy()
+    e_gpu, e_cpu = np.abs(got[0, :, :vl] - exact), np.abs(cpu_out[0, :, :vl] - exact)
+    return {"f64_sample": "sequence 0, every head, against torch float64 on the host",
+            "gpu_vs_f64_max_abs": float(e_gpu.max()), "cpu_vs_f64_max_abs": float(e_cpu.max()),
+            "gpu_vs_f64_rms": float(np.sqrt((e_gpu ** 2).mean())),
+            "cpu_vs_f64_rms": float(np.sqrt((e_cpu ** 2).mean()))}
+
+
 # --- one attention workload ---------------------------------------------------------------------
 
 def attention_line(name: str, steps: int, warmup: int, cpu_seconds: float, cpu: bool) -> dict:
@@ -376,6 +404,8 @@ def attention_line(name: str, steps: int, warmup: int, cpu_seconds: float, cpu: 
                 raise RuntimeError(f"{name}: the input copies gave different outputs")
         cb["gpu_vs_cpu_max_abs"] = max(float(np.abs(got[i, :, : valid[i]] - cpu_out[i, :, : valid[i]]).max())
                                        for i in range(b))
+        if wl["outliers"] and wl["mask"][0] in ("block_diag", "block3"):
+            cb.update(f64_errors(qkv, valid, wl, got, cpu_out))
         line["cpu_baseline"] = cb
     line["_tensors"] = (q, k, v, out, vl, mask, stream)
     return line
@@ -929,6 +959,10 @@ def compact(result: dict) -> dict:
         if "cpu_baseline" in ln:
             e["cpu_tflops"] = _r(ln["cpu_baseline"]["value"])
             e["max_abs"] = _r(ln["cpu_baseline"]["gpu_vs_cpu_max_abs"], 2)
+            if "gpu_vs_f64_max_abs" in ln["cpu_baseline"]:  # [GPU, CPU port] against float64
+                lb = ln["cpu_baseline"]
+                e["f64_max_abs"] = [_r(lb["gpu_vs_f64_max_abs"], 2), _r(lb["cpu_vs_f64_max_abs"], 2)]
+                e["f64_rms"] = [_r(lb["gpu_vs_f64_rms"], 2), _r(lb["cpu_vs_f64_rms"], 2)]
             if "naive_t1_value" in ln["cpu_baseline"]:
                 e["cpu_naive_t1_tflops"] = _r(ln["cpu_baseline"]["naive_t1_value"])
         lines[name] = e
