@@ -22,6 +22,7 @@
 // also apply rotary embedding (ops.rs:118-141) to the q and k sections of a
 // packed QKV projection, so encoder::attend's split_qkv + rope_in_place pass
 // (encoder.rs:36-71) is not needed.
+#include <algorithm>
 #include <type_traits>
 
 #include "internal.hpp"
@@ -239,14 +240,16 @@ __global__ void __launch_bounds__(kThreads) gemm_nt_kernel(const GemmLaunch g) {
 
 
 // The ring kernel: k a multiple of 16, 16-byte aligned operands with row
-// strides a multiple of 4 floats.  Slabs of 16 k go from HBM straight into a
-// 3-stage LDS ring (global_load_lds_dwordx4, no staging registers), two slabs
-// ahead of the MFMAs, with one barrier per slab.  The DMA is issued from asm
-// with explicit vmcnt waits: the compiler cannot tell the ring's stages apart
-// and would otherwise wait for every DMA before each LDS read.  Rows past m
-// (or past b's rows) load a clamped in-range row; the epilogue drops them.
+// strides a multiple of 4 floats.  Slabs of 16 k go from HBM straight into an
+// LDS ring (global_load_lds_dwordx4, no staging registers) with one barrier per
+// slab.  Two ring depths: 2 stages, one slab ahead of the MFMAs, 37 KB of LDS and
+// at most 128 VGPRs, so 4 workgroups share a CU; or 3 stages, two slabs ahead,
+// 48 KB and 3 workgroups per CU, for the split-K launches (short K loops on small
+// grids) and the folded LayerNorm (whose centring needs more registers).  The DMA
+// is issued from asm with explicit vmcnt waits: the compiler cannot tell the
+// ring's stages apart and would otherwise wait for every DMA before each LDS read.
+// Rows past m (or past b's rows) load a clamped in-range row; the epilogue drops them.
 constexpr int RBK = 16;       // k per slab
-constexpr int RSTAGES = 3;    // LDS ring depth
 constexpr int kTileFloats = BM * RBK;  // one operand tile of one stage (8 KB)
 
 // 16-byte chunk c (0..3) of tile row r sits at chunk c ^ rswz(r) of the row:
@@ -452,11 +455,14 @@ __device__ __forceinline__ void epilogue_staged(const GemmLaunch &g, floatx16 (&
 __device__ __forceinline__ float norm_centre(float4 st) { return fabsf(st.x) * st.z > 1.0f ? st.x : 0.0f; }
 
 // NORM: the input rows' LayerNorm is folded in (GemmLaunch::in_stats); STATS:
-// the output rows' chunk statistics are written (GemmLaunch::out_stats).
-template <int ACT, bool ROPE, bool NORM = false, bool STATS = false>
-__global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch g) {
-    __shared__ __attribute__((aligned(16))) float ring[RSTAGES * 2 * kTileFloats];  // 48 KB
-    static_assert(4 * kStageFloats + 2 * BM <= RSTAGES * 2 * kTileFloats, "epilogue staging and row statistics fit the ring");
+// the output rows' chunk statistics are written (GemmLaunch::out_stats); DEEP: the
+// 3-stage ring (taken with NORM too).
+template <int ACT, bool ROPE, bool NORM = false, bool STATS = false, bool DEEP = false>
+__global__ void __launch_bounds__(kThreads, NORM || DEEP ? 3 : 4) gemm_ring_kernel(const GemmLaunch g) {
+    constexpr int RSTAGES = NORM || DEEP ? 3 : 2;
+    // The ring, also the epilogue's staging and row statistics once the K loop is done.
+    constexpr int kRingFloats = std::max(RSTAGES * 2 * kTileFloats, 4 * kStageFloats + 2 * BM);
+    __shared__ __attribute__((aligned(16))) float ring[kRingFloats];  // 48 KB or 37 KB
 
     constexpr bool GEGLU = ACT == RAYA_EPI_GEGLU;
     constexpr int OUT_BN = GEGLU ? BN / 2 : BN;
@@ -561,21 +567,26 @@ __global__ void __launch_bounds__(kThreads, 3) gemm_ring_kernel(const GemmLaunch
       const auto kloop = [&](auto centre_tag) {
         constexpr bool C = decltype(centre_tag)::value;
         issue(0, 0);
-        if (nk > 1) issue(1, 1);
+        if (RSTAGES == 3 && nk > 1) issue(1, 1);
         int stage = 0;
         for (int kt = 0; kt < nk; ++kt) {
-            // Each wave issued 4 DMAs per slab: with slab kt + 1 in flight, vmcnt(4)
-            // means slab kt has landed; the barrier makes that hold for every wave and
-            // retires the reads of the stage slab kt + 2 goes into.
-            if (kt + 1 < nk)
+            // Each wave issues 4 DMAs per slab.  3 stages: with slab kt + 1 in flight,
+            // vmcnt(4) means slab kt has landed; 2 stages: slab kt is the only one in
+            // flight.  The barrier makes that hold for every wave and retires the reads
+            // of the stage the next issue goes into (slab kt - 1's).
+            if (RSTAGES == 3 && kt + 1 < nk)
                 asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
             else
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             barrier_only();
-            if (kt + 2 < nk) issue(kt + 2, stage == 0 ? 2 : stage - 1);
+            if constexpr (RSTAGES == 3) {
+                if (kt + 2 < nk) issue(kt + 2, stage == 0 ? 2 : stage - 1);
+            } else {
+                if (kt + 1 < nk) issue(kt + 1, stage ^ 1);
+            }
             // The slab's operand reads and MFMAs run at raised wave priority, so a
             // wave that has passed its barrier keeps the matrix core busy while the
-            // other workgroups' waves wait at theirs: the three workgroups of a CU
+            // other workgroups' waves wait at theirs: the workgroups of a CU
             // drift out of step instead of stalling together (+2-5% on the encoder
             // shapes against equal priority).
             __builtin_amdgcn_s_setprio(1);
@@ -687,7 +698,9 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
     }
     if (ring_ok) {
         constexpr bool NONE = ACT == RAYA_EPI_NONE;
-        const auto ring = [&](const GemmLaunch &gg, dim3 gr) -> hipError_t {
+        // Split-K launches (small grids, short K loops) take the 3-stage ring.
+        const auto ring_depth = [&](const GemmLaunch &gg, dim3 gr, auto deep_tag) -> hipError_t {
+            constexpr bool D = decltype(deep_tag)::value;
             if (gg.in_stats) {  // folded LayerNorm: QKV (with or without RoPE) and GeGLU
                 if (gg.rope_cos)
                     hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE, true>), gr, block, 0, stream, gg);
@@ -695,15 +708,18 @@ hipError_t launch_act(const GemmLaunch &g, hipStream_t stream) {
                     hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, true>), gr, block, 0, stream, gg);
             } else if (gg.out_stats) {  // the residual GEMMs
                 if constexpr (NONE)
-                    hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, false, true>), gr, block, 0, stream, gg);
+                    hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, false, true, D>), gr, block, 0, stream, gg);
                 else
                     return hipErrorInvalidValue;
             } else if (gg.rope_cos) {
-                hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE>), gr, block, 0, stream, gg);
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, NONE, false, false, D>), gr, block, 0, stream, gg);
             } else {
-                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false>), gr, block, 0, stream, gg);
+                hipLaunchKernelGGL((gemm_ring_kernel<ACT, false, false, false, D>), gr, block, 0, stream, gg);
             }
             return hipGetLastError();
+        };
+        const auto ring = [&](const GemmLaunch &gg, dim3 gr) -> hipError_t {
+            return splits > 1 ? ring_depth(gg, gr, std::true_type{}) : ring_depth(gg, gr, std::false_type{});
         };
         hipError_t e = ring(g, grid);
         if (e != hipSuccess || splits == 1) return e;
