@@ -812,21 +812,41 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     float l = 0.f;        // this lane's partial sum of weights
 
     if constexpr (TIMED) clk->last = clock_now();
-    // The whole-item prefetch runs its steps to MAXT, fully unrolled (its register
-    // sets are indexed by the step); the steps past the item's tiles idle.
-#pragma unroll kUnroll
-    for (int j = 0; j < (ALL ? kUnroll : n_tiles); ++j) {
+    if constexpr (ALL) {
+        // Every tile's operands are in registers: the scores of step j + 1 go to the
+        // matrix core before the softmax of step j, which runs beside them.  The steps
+        // run to MAXT, fully unrolled (the register sets are indexed by the step);
+        // those past the item's tiles are neither scored nor accumulated.
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const bool in = qi < valid;  // Q as below: zero past valid, negated for a negative scale
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qreg[4 * c + e] = in ? qreg[4 * c + e] * q_sign : 0.f;
+        }
+        floatx4 s_cur = qk_regs(kall[0], qreg);
+#pragma unroll
+        for (int j = 0; j < kUnroll; ++j) {
+            floatx4 s_nxt;
+            if (j + 1 < kUnroll && j + 1 < n_tiles) s_nxt = qk_regs(kall[j + 1], qreg);
+            const int kt = tile_at(j);
+            const int k16 = kt + 16 * wave;  // this wave's subtile, as `live` below
+            const bool active = wave_live && j < n_tiles && kt < w_last.hi && kt + kKeys > w_first.lo &&
+                                k16 < w_last.hi && k16 + 16 > w_first.lo;
+            if (active) {
+                const int m_lo = max(rr.lo, k16), m_hi = min(rr.hi, k16 + 16);
+                softmax_sub<NT>(s_cur, oacc, m, l, wave, m_lo - kt - g, m_hi - kt - g, c_exp);
+                pv_regs(vall[j], s_cur, oacc);
+            }
+            if (j + 1 < kUnroll) s_cur = s_nxt;
+        }
+    } else {
+#pragma unroll 1
+    for (int j = 0; j < n_tiles; ++j) {
         const int kt = tile_at(j);
         int kx, ky;
         step_keys(kt, kx, ky);
         float4 knext[4], vnext[4];
-        if constexpr (ALL) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                kcur[c] = kall[j][c];
-                vcur[c] = vall[j][c];
-            }
-        } else if constexpr (DIRECT) {
+        if constexpr (DIRECT) {
             if (j + 1 < n_tiles) load_sub(tile_at(j + 1), knext, vnext);
         }
         if (!DIRECT && j != 0) {
@@ -855,7 +875,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 for (int e = 0; e < 4; ++e) qreg[4 * c + e] = in ? qreg[4 * c + e] * q_sign : 0.f;
             }
         }
-        bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo && (!ALL || j < n_tiles);
+        bool rows_active = wave_live && kt < w_last.hi && kt + kKeys > w_first.lo;
         // Sliding windows: the 16-key subtiles outside the union of the wave's
         // key intervals [w_first.lo, w_last.hi) hold no live key for any of its
         // rows (about a quarter of an item's subtiles at Window64); such a tile
@@ -936,7 +956,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 lap(clk, clk->pv);
             }
         }
-        if constexpr (DIRECT && !ALL) {
+        if constexpr (DIRECT) {
             if (j + 1 < n_tiles) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -945,6 +965,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 }
             }
         }
+    }
     }
     l = sum_xor32(sum_xor16(l));
 
