@@ -515,6 +515,13 @@ __device__ __forceinline__ floatx4 qk_regs(const float4 (&k)[4], const float (&q
     }
     return acc;
 }
+// Zeroes the rows of a register subtile (v[r]: key k0 + 4r + g) at or past k_hi, which
+// were loaded as copies of the item's last key: they weigh 0, and 0 * Inf would be NaN.
+__device__ __forceinline__ void zero_past(float4 (&v)[4], int k0, int g, int k_hi) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (k0 + 4 * r + g >= k_hi) v[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
 __device__ __forceinline__ void pv_regs(const float4 (&v)[4], const floatx4 &s, floatx4 (&oacc)[4]) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -835,6 +842,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             if (active) {
                 const int m_lo = max(rr.lo, k16), m_hi = min(rr.hi, k16 + 16);
                 softmax_sub<NT>(s_cur, oacc, m, l, wave, m_lo - kt - g, m_hi - kt - g, c_exp);
+                if (kt + kKeys > it.k_hi) zero_past(vall[j], k16, g, it.k_hi);
                 pv_regs(vall[j], s_cur, oacc);
             }
             if (j + 1 < kUnroll) s_cur = s_nxt;
@@ -941,16 +949,34 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         }
         if constexpr (!DIRECT) {
             __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's V loads have landed
+            // Rows past the item's last key were loaded as copies of it: they weigh 0, but
+            // 0 * Inf is NaN, so a non-finite V at that key would reach rows that do not
+            // see the copies.  This wave zeroes its own chunks of them before PV.  (Under
+            // the sliding masks keys inside a scored subtile but outside a row's window
+            // weigh 0 the same way; there the copies change nothing.)
+            if (!SKIP && max(kx, ky) + kKeys > it.k_hi) {
+                int ln = lane;
+                asm volatile("" : "+v"(ln));  // keeps this rare path's arithmetic inside it
+#pragma unroll
+                for (int jj = 0; jj < LPW; ++jj) {
+                    const int lrow = ((wave * LPW + jj) * 64 + ln) / CH;
+                    if (((lrow >> 4) & 1 ? ky : kx) + lrow >= it.k_hi)
+                        *(float4 *)((char *)vs + (wave * LPW + jj) * 1024 + ln * 16) = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zeros are in LDS
+            }
             barrier_only();
         }
         if constexpr (TIMED) lap(clk, clk->load_wait);
         if (active) {
-            if constexpr (DIRECT)
+            if constexpr (DIRECT) {
+                if (kt + kKeys > it.k_hi) zero_past(vcur, kt + 16 * wave, g, it.k_hi);
                 pv_regs(vcur, ssub, oacc);
-            else if constexpr (SPLIT)
+            } else if constexpr (SPLIT) {
                 pv_sub<DP>(vs, ssub, g, li, oacc, wave);
-            else
+            } else {
                 pv_tile<DP>(vs, sacc, g, li, oacc, live);
+            }
             if constexpr (TIMED) {
                 settle(oacc);
                 lap(clk, clk->pv);

@@ -584,6 +584,31 @@ def test_non_finite_v_outside_a_window(hip_attention):
         print(f"{mask.name()}: {int((~same).sum())} of {gc.size} rows outside the window are NaN in dim {c}")
 
 
+@pytest.mark.parametrize("name", ["block3", "full", "block_diag64", "block_diag128"])
+def test_non_finite_v_at_the_last_valid_key(hip_attention, name):
+    """+Inf and NaN in V at the last valid key (naive.rs:13-65 sums each row over its own
+    range): rows whose range holds that key are +Inf (NaN) in that dim, every other output
+    matches the oracle.  The kernels load keys past the item's last one as copies of it, at
+    weight 0, and zero them before PV, so the copies add nothing (0 * Inf would be NaN).
+    Valid lengths ending mid-subtile (392) and on a subtile edge (400)."""
+    mask, okind, block, window = MASKS[name]
+    h, s, d, c = 2, 512, 64, 5
+    q, k, v = oracle.qkv(h, s, d, 93)
+    for valid in (392, 400):
+        for bad in (np.inf, np.nan):
+            vv = v.copy()
+            vv[:, valid - 1, c] = bad
+            got = run_hip(hip_attention, q, k, vv, mask, valid, fill=7.0)
+            want = oracle_naive(q, k, vv, okind, valid, block, window)
+            assert (got[:, valid:] == 0).all()
+            g, w = got[:, :valid], want[:, :valid]
+            assert (np.isnan(g) == np.isnan(w)).all(), (valid, bad)
+            assert (np.isinf(g) == np.isinf(w)).all() and (g[np.isinf(w)] == w[np.isinf(w)]).all(), (valid, bad)
+            assert (~np.isfinite(w)).any()
+            fin = np.isfinite(w)
+            assert np.abs(g[fin] - w[fin]).max() < MAX_ABS, (valid, bad)
+
+
 @pytest.mark.parametrize("name", ["block3", "window64", "full", "block_diag64", "sliding8"])
 def test_non_finite_scores_match_the_reference(hip_attention, name):
     """NaN and Inf in Q and K against the restated Naive kernel (naive.rs:13-65): a NaN in one
