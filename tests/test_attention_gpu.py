@@ -584,15 +584,17 @@ def test_non_finite_v_outside_a_window(hip_attention):
         print(f"{mask.name()}: {int((~same).sum())} of {gc.size} rows outside the window are NaN in dim {c}")
 
 
+@pytest.mark.parametrize("d", [64, 40, 128])
 @pytest.mark.parametrize("name", ["block3", "full", "block_diag64", "block_diag128"])
-def test_non_finite_v_at_the_last_valid_key(hip_attention, name):
+def test_non_finite_v_at_the_last_valid_key(hip_attention, name, d):
     """+Inf and NaN in V at the last valid key (naive.rs:13-65 sums each row over its own
     range): rows whose range holds that key are +Inf (NaN) in that dim, every other output
     matches the oracle.  The kernels load keys past the item's last one as copies of it, at
     weight 0, and zero them before PV, so the copies add nothing (0 * Inf would be NaN).
-    Valid lengths ending mid-subtile (392) and on a subtile edge (400)."""
+    Valid lengths ending mid-subtile (392) and on a subtile edge (400); head_dim 64 (the
+    fused kernels) and 40, 128 (the general ones)."""
     mask, okind, block, window = MASKS[name]
-    h, s, d, c = 2, 512, 64, 5
+    h, s, c = 2, 512, 5
     q, k, v = oracle.qkv(h, s, d, 93)
     for valid in (392, 400):
         for bad in (np.inf, np.nan):
