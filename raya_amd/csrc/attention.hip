@@ -954,7 +954,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
             // see the copies.  This wave zeroes its own chunks of them before PV.  (Under
             // the sliding masks keys inside a scored subtile but outside a row's window
             // weigh 0 the same way; there the copies change nothing.)
-            if (!SKIP && max(kx, ky) + kKeys > it.k_hi) {
+            if ((!SKIP || MK == RAYA_MASK_BLOCKDIAG) && max(kx, ky) + kKeys > it.k_hi) {
                 int ln = lane;
                 asm volatile("" : "+v"(ln));  // keeps this rare path's arithmetic inside it
 #pragma unroll
@@ -1115,12 +1115,15 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_kernel(const A
 // and the mask is known, so the item decode and key ranges compile to a few
 // scalar instructions (the general kernel's first K/V load sits behind the
 // decode of every mask kind and the tile walk's set-up): 64 VGPRs instead of
-// 126, and the first load about 420 instructions earlier.
-template <int DP>
+// 126, and the first load about 420 instructions earlier.  Blocks narrower than 64
+// (SKIP) leave each wave's rows whole 16-key subtiles of other blocks' keys, which it
+// skips: a quarter (b <= 16) or half (b = 32) of the matrix work, and no other block's
+// V enters its rows even at weight 0 (0 * Inf would be NaN) when b is 16 or 32.
+template <int DP, bool SKIP>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_blockdiag_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, true, false, false, false, RAYA_MASK_BLOCKDIAG, true>(a, p, ks, vs, nullptr);
+    attend_body<DP, true, false, SKIP, false, RAYA_MASK_BLOCKDIAG, true>(a, p, ks, vs, nullptr);
 }
 
 template <int DP, int MK>
@@ -1279,8 +1282,10 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
             hipLaunchKernelGGL((attend_sliding_kernel<DP, RAYA_MASK_WINDOW64>), grid, block, 0, stream, a, p);
         else if (sliding)
             hipLaunchKernelGGL((attend_sliding_kernel<DP, RAYA_MASK_SLIDING>), grid, block, 0, stream, a, p);
+        else if (a.mask_kind == RAYA_MASK_BLOCKDIAG && a.mask_arg == kKeys)
+            hipLaunchKernelGGL((attend_blockdiag_kernel<DP, false>), grid, block, 0, stream, a, p);
         else if (a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
-            hipLaunchKernelGGL((attend_blockdiag_kernel<DP>), grid, block, 0, stream, a, p);
+            hipLaunchKernelGGL((attend_blockdiag_kernel<DP, true>), grid, block, 0, stream, a, p);
         else
             hipLaunchKernelGGL((attend_kernel<DP, true>), grid, block, 0, stream, a, p);
     } else {

@@ -611,6 +611,27 @@ def test_non_finite_v_at_the_last_valid_key(hip_attention, name, d):
             assert np.abs(g[fin] - w[fin]).max() < MAX_ABS, (valid, bad)
 
 
+@pytest.mark.parametrize("b", [16, 32])
+def test_non_finite_v_under_narrow_blocks(hip_attention, b):
+    """BlockDiag(16) and (32): an Inf or NaN in V at key j reaches exactly the rows of j's block
+    (a 64-key tile holds other blocks' keys, whose 16-key subtiles each wave skips), every other
+    output matches the oracle."""
+    h, s, d, valid, c = 2, 320, 64, 301, 7
+    q, k, v = oracle.qkv(h, s, d, 95)
+    for j in (37, 100, 300):
+        for bad in (np.inf, -np.inf, np.nan):
+            vv = v.copy()
+            vv[:, j, c] = bad
+            got = run_hip(hip_attention, q, k, vv, R.Mask.block_diag(b), valid)
+            want = oracle_naive(q, k, vv, oracle.MASK_BLOCKDIAG, valid, b, 0)
+            assert (got[:, valid:] == 0).all()
+            g, w = got[:, :valid], want[:, :valid]
+            assert (np.isnan(g) == np.isnan(w)).all(), (b, j, bad)
+            assert (np.isinf(g) == np.isinf(w)).all() and (g[np.isinf(w)] == w[np.isinf(w)]).all(), (b, j, bad)
+            fin = np.isfinite(w)
+            assert np.abs(g[fin] - w[fin]).max() < MAX_ABS, (b, j, bad)
+
+
 @pytest.mark.parametrize("name", ["block3", "window64", "full", "block_diag64", "sliding8"])
 def test_non_finite_scores_match_the_reference(hip_attention, name):
     """NaN and Inf in Q and K against the restated Naive kernel (naive.rs:13-65): a NaN in one
