@@ -72,6 +72,8 @@ struct Plan {
     FastDiv by_qt, by_heads, by_arg;  // by_arg: the BlockDiag width (1 otherwise)
     int pairs_per_xcd;                 // > 0: whole (sequence, head) pairs per XCD
     int quads;                         // split kernel: each 4 consecutive items on one XCD
+    int rot_units, rot_shift;          // > 0: units of 2^rot_shift tiles dealt round the XCDs
+    FastDiv by_rot;                    // by rot_units << rot_shift (items of a pair per XCD)
 };
 
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroup i runs on XCD i mod 8
@@ -177,19 +179,30 @@ __device__ __forceinline__ float sum_xor32(float x) {
 
 __device__ __forceinline__ int scatter(int i, int total, int half_bits);
 
-// The item workgroup `bid` computes.  When the number of (sequence, head)
-// pairs is a multiple of the XCD count, XCD x takes pairs x, x + 8, x + 16, ...
-// and walks each one tile by tile: the workgroups running together on an XCD
-// read neighbouring rows (DRAM pages stay open; overlapping key ranges of
-// Block3 and Sliding hit in that XCD's L2), while the heads of each sequence,
-// and with them its padding, spread over all XCDs.  Otherwise a scattered
-// order.
+// The item workgroup `bid` computes.  With rot_units > 0 (the 64-row kernels
+// under Block3 and BlockDiag wider than a tile), each (sequence, head) pair's tiles
+// form units of 2^rot_shift consecutive tiles dealt round the XCDs, rotated by
+// the pair's index, and every XCD walks the pairs in order: each XCD holds an
+// equal share of every pair's valid rows, and a unit's items share their key
+// tiles in one L2.  Otherwise, when the number of pairs is a multiple of the
+// XCD count, XCD x takes pairs x, x + 8, x + 16, ... and walks each one tile by
+// tile: the workgroups running together on an XCD read neighbouring rows (DRAM
+// pages stay open; overlapping key ranges of Block3 and Sliding hit in that
+// XCD's L2), while the heads of each sequence, and with them its padding,
+// spread over all XCDs.  Otherwise a scattered order.
 //
 // The split kernel's items are 16-row tiles: when the pairs do not divide
 // among the XCDs, every four consecutive items (the 16-row tiles of one 64-row
 // block, which share their key tiles) still go to one XCD, so that block's K/V
 // is fetched into one L2 once rather than into four.
 __device__ __forceinline__ int item_of(int bid, const Plan &p) {
+    if (p.rot_units > 0) {  // n_qt = 8 rot_units 2^rot_shift
+        const int x = bid % kXcds, s = bid / kXcds;
+        const int pair = fdiv(s, p.by_rot);
+        const int r = s - pair * (p.rot_units << p.rot_shift);
+        const int unit = kXcds * (r >> p.rot_shift) + ((x - pair) & (kXcds - 1));
+        return pair * p.n_qt + (unit << p.rot_shift) + (r & ((1 << p.rot_shift) - 1));
+    }
     if (p.pairs_per_xcd > 0) {
         const int x = bid % kXcds, j = bid / kXcds;
         const int pj = fdiv(j, p.by_qt);
@@ -1233,6 +1246,35 @@ bool prefetch_all() {
     return !(e && !std::strcmp(e, "0"));
 }
 
+// Item order of the 64-row kernels.  XCD x taking whole (sequence, head) pairs
+// gives each XCD the padding of the sequences whose heads it holds: with 12
+// heads on 8 XCDs, even sequences put two heads on XCDs 0-3 and odd ones on
+// XCDs 4-7, so the XCDs' shares of the work differ by the two halves' valid
+// lengths (7% on a batch of 32 sequences of U[512, 2048] valid rows).  Dealing
+// each pair's units of 4 consecutive tiles round the XCDs, rotated by the
+// pair's index, gives every XCD an equal share of every pair while a unit's
+// items still share their key tiles in one L2: the MFMA-bound multi-tile lines
+// gain about 1% (Block3 and BlockDiag(128) at 4 x 12 x 16384, Block3 at 32 x
+// 12 x 2048).  Single-tile BlockDiag(b <= 64) keeps whole pairs: HBM-bound, it
+// runs the same either way (the XCD that finishes early leaves its bandwidth
+// to the others), and units of 1 or 2 tiles, which scatter neighbouring rows
+// over the XCDs, run it 16-20% slower.  Window64 and Sliding keep whole pairs
+// too (units of 4 tiles: 0.4-1.5% slower on 16 heads x 4096 and 8192 rows).  RAYA_ATTN_ORDER=pairs keeps whole
+// pairs, rot1/rot2/rot4/rot8 deal units of that many tiles for any mask; the
+// units must divide a pair's tiles 8 times over, else whole pairs.  Returns
+// the shift, or -1 for whole pairs.
+int rotate_shift(const AttnLaunch &a) {
+    if (const char *e = std::getenv("RAYA_ATTN_ORDER")) {
+        if (!std::strcmp(e, "pairs")) return -1;
+        if (!std::strcmp(e, "rot1")) return 0;
+        if (!std::strcmp(e, "rot2")) return 1;
+        if (!std::strcmp(e, "rot4")) return 2;
+        if (!std::strcmp(e, "rot8")) return 3;
+    }
+    const bool wide_block = a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg != 0;
+    return a.mask_kind == RAYA_MASK_BLOCK3 || wide_block ? 2 : -1;
+}
+
 template <int DP, bool FUSED = false>
 hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const bool split = use_split(a);
@@ -1250,6 +1292,14 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const int64_t pairs = (int64_t)a.heads * a.batch;
     p.pairs_per_xcd = pairs % kXcds == 0 ? (int)(pairs / kXcds) : 0;
     p.quads = split && p.pairs_per_xcd == 0 && total % (4 * kXcds) == 0;
+    p.rot_units = p.rot_shift = 0;
+    p.by_rot = make_fastdiv(1u);
+    const int shift = split ? -1 : rotate_shift(a);
+    if (shift >= 0 && n_qt % (kXcds << shift) == 0) {
+        p.rot_shift = shift;
+        p.rot_units = (int)(n_qt / (kXcds << shift));
+        p.by_rot = make_fastdiv((uint32_t)(p.rot_units << shift));
+    }
     const dim3 grid((unsigned)total), block(kThreads);
     const bool sliding = a.mask_kind == RAYA_MASK_SLIDING || a.mask_kind == RAYA_MASK_WINDOW64;
     if (split) {

@@ -197,6 +197,36 @@ def test_batched_device_path_dense_and_strided(hip_attention):
         check_close(ctx.cpu().numpy().transpose(0, 2, 1, 3), want, f"strided {name}")
 
 
+@pytest.mark.parametrize("seq", [4096, 2000])
+@pytest.mark.parametrize("name", ["block_diag64", "block_diag128", "block3", "window64"])
+def test_item_orders_give_identical_outputs(hip_attention, monkeypatch, name, seq):
+    """RAYA_ATTN_ORDER only changes which workgroup computes which item: whole (sequence, head)
+    pairs per XCD, or each pair's units of 1, 2, 4 or 8 tiles dealt round the XCDs.  Every
+    order gives the same bits, within the bar of the oracle.  4 sequences x 2 heads x 4096
+    rows (64 tiles of 64 rows: every unit size divides them) and x 2000 rows (32 tiles
+    rounded up, the last one partial: units of 8 do not divide them, which keeps whole
+    pairs)."""
+    b, h, d = 4, 2, 64
+    valid = np.array([seq, seq - 700, seq // 2 + 13, 1], np.int32)
+    q, k, v = (synth.normal(31 + i, b * h * seq * d).reshape(b, h, seq, d) for i in range(3))
+    mask, okind, block, window = MASKS[name]
+    want = oracle.naive_attend_batched(q, k, v, okind, valid, R.kernels.default_scale(d),
+                                       block=block, window=window)
+    outs = {}
+    for order in ("pairs", "rot1", "rot2", "rot4", "rot8", None):
+        if order is None:
+            monkeypatch.delenv("RAYA_ATTN_ORDER", raising=False)
+        else:
+            monkeypatch.setenv("RAYA_ATTN_ORDER", order)
+        out = torch.full((b, h, seq, d), 5.0, device="cuda")
+        hip_attention.attend_batched(_dev(q), _dev(k), _dev(v), out, _dev(valid), mask)
+        torch.cuda.synchronize()
+        outs[order] = out.cpu().numpy()
+    check_close(outs[None], want, f"{name} default order")
+    for order, got in outs.items():
+        assert np.array_equal(got, outs[None]), f"{name}: order {order} differs from the default"
+
+
 @pytest.mark.parametrize("width", [1, 2, 4, 8, 16, 32, 64, 48, 96])
 def test_block_diag_widths_dense_and_strided(hip_attention, width):
     """BlockDiag(b) at head_dim 64 for every b dividing 64 (the single-tile kernels, mask
