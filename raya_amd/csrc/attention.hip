@@ -71,7 +71,7 @@ struct Plan {
     int total, half_bits, n_qt;
     FastDiv by_qt, by_heads, by_arg;  // by_arg: the BlockDiag width (1 otherwise)
     int pairs_per_xcd;                 // > 0: whole (sequence, head) pairs per XCD
-    int quads;                         // split kernel: each 4 consecutive items on one XCD
+    int quads;                         // split kernel: each 4 consecutive items on one XCD (2: rotated)
     int rot_units, rot_shift;          // > 0: units of 2^rot_shift tiles dealt round the XCDs
     FastDiv by_rot;                    // by rot_units << rot_shift (items of a pair per XCD)
 };
@@ -194,7 +194,14 @@ __device__ __forceinline__ int scatter(int i, int total, int half_bits);
 // The split kernel's items are 16-row tiles: when the pairs do not divide
 // among the XCDs, every four consecutive items (the 16-row tiles of one 64-row
 // block, which share their key tiles) still go to one XCD, so that block's K/V
-// is fetched into one L2 once rather than into four.
+// is fetched into one L2 once rather than into four.  XCD x takes the k-th of
+// each run of 8 such quads rotated by 2k (quads = 2): with 8 quads per
+// (sequence, head) pair, XCD x would otherwise always take 64-row block x of
+// every head, and under Block3 at L = 512 the blocks in the middle span 6 tiles
+// and the outer ones 4, so XCDs 2-5 held 1.5 times the work of the others;
+// rotated, every XCD takes all four even or all four odd blocks of every four
+// heads.  (One sequence of 12 x 512 under Block3: 15.27 -> 15.13 us;
+// RAYA_ATTN_QUADS=plain keeps the unrotated order.)
 __device__ __forceinline__ int item_of(int bid, const Plan &p) {
     if (p.rot_units > 0) {  // n_qt = 8 rot_units 2^rot_shift
         const int x = bid % kXcds, s = bid / kXcds;
@@ -209,8 +216,9 @@ __device__ __forceinline__ int item_of(int bid, const Plan &p) {
         return (pj * kXcds + x) * p.n_qt + (j - pj * p.n_qt);
     }
     if (p.quads) {  // total is a multiple of 4 * kXcds
-        const int x = bid % kXcds, j = bid / kXcds;
-        return ((j >> 2) * kXcds + x) * 4 + (j & 3);
+        const int x = bid % kXcds, j = bid / kXcds, k = j >> 2;
+        const int xr = p.quads > 1 ? (x + 2 * k) & (kXcds - 1) : x;
+        return (k * kXcds + xr) * 4 + (j & 3);
     }
     return scatter(bid, p.total, p.half_bits);
 }
@@ -1292,6 +1300,10 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const int64_t pairs = (int64_t)a.heads * a.batch;
     p.pairs_per_xcd = pairs % kXcds == 0 ? (int)(pairs / kXcds) : 0;
     p.quads = split && p.pairs_per_xcd == 0 && total % (4 * kXcds) == 0;
+    if (p.quads) {
+        const char *e = std::getenv("RAYA_ATTN_QUADS");
+        if (!(e && !std::strcmp(e, "plain"))) p.quads = 2;
+    }
     p.rot_units = p.rot_shift = 0;
     p.by_rot = make_fastdiv(1u);
     const int shift = split ? -1 : rotate_shift(a);

@@ -227,6 +227,23 @@ def test_item_orders_give_identical_outputs(hip_attention, monkeypatch, name, se
         assert np.array_equal(got, outs[None]), f"{name}: order {order} differs from the default"
 
 
+@pytest.mark.parametrize("name", ["block3", "block_diag64", "window64"])
+def test_quad_orders_give_identical_outputs(hip_attention, monkeypatch, name):
+    """One sequence of 12 heads x 512 rows (12 pairs, not a multiple of the 8 XCDs): the
+    16-row items go round the XCDs in quads, rotated by default, in order with
+    RAYA_ATTN_QUADS=plain.  Same bits either way, within the bar of the oracle."""
+    h, s, d, valid = 12, 512, 64, 500
+    q, k, v = oracle.qkv(h, s, d, 61)
+    mask, okind, block, window = MASKS[name]
+    want = oracle_naive(q, k, v, okind, valid, block, window)
+    monkeypatch.setenv("RAYA_ATTN_QUADS", "plain")
+    plain = run_hip(hip_attention, q, k, v, mask, valid)
+    monkeypatch.delenv("RAYA_ATTN_QUADS")
+    rot = run_hip(hip_attention, q, k, v, mask, valid)
+    check_close(rot, want, f"{name} rotated quads")
+    assert np.array_equal(plain, rot)
+
+
 @pytest.mark.parametrize("width", [1, 2, 4, 8, 16, 32, 64, 48, 96])
 def test_block_diag_widths_dense_and_strided(hip_attention, width):
     """BlockDiag(b) at head_dim 64 for every b dividing 64 (the single-tile kernels, mask
