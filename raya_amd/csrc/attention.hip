@@ -445,6 +445,59 @@ __device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4
     }
 }
 
+// Non-finite V under masks whose key ranges differ between the rows of a wave
+// (Window64, Sliding, BlockDiag of a width that 16 does not divide).  A 16-key
+// subtile cut by some row's range gives that row weight 0 at the keys outside
+// it, and the matrix core multiplies those zeros by V: 0 * Inf is NaN where
+// Naive::attend sums each row over its own range only (naive.rs:13-65).  Such a
+// NaN can only appear in a row whose output is not finite, so under these masks
+// each non-finite output chunk is recomputed here, in Naive's order and over the
+// row's own key range: 4 dims d0 .. d0 + 3 of the row with Q row qrow, from HBM
+// (the path only runs on non-finite inputs).  Scores are the dot product in dim
+// order times the scale; the maximum ignores NaN scores as the reference's
+// f32::max does, and a NaN or +Inf score makes the row NaN through the sum.
+__device__ __forceinline__ float4 exact_chunk(const float *qrow, const float *kb, int64_t k_rs,
+                                                        const float *vb, int64_t v_rs, int lo, int hi, int D,
+                                                        float scale, int d0) {
+    float mx = -INFINITY;
+#pragma unroll 1
+    for (int j = lo; j < hi; ++j) {
+        const float *krow = kb + (int64_t)j * k_rs;
+        float s = 0.f;
+#pragma unroll 1
+        for (int d = 0; d < D; ++d) s = __fadd_rn(s, __fmul_rn(qrow[d], krow[d]));
+        mx = fmaxf(mx, __fmul_rn(s, scale));
+    }
+    float sum = 0.f;
+#pragma unroll 1
+    for (int j = lo; j < hi; ++j) {
+        const float *krow = kb + (int64_t)j * k_rs;
+        float s = 0.f;
+#pragma unroll 1
+        for (int d = 0; d < D; ++d) s = __fadd_rn(s, __fmul_rn(qrow[d], krow[d]));
+        sum = __fadd_rn(sum, expf(__fmul_rn(s, scale) - mx));
+    }
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+    for (int j = lo; j < hi; ++j) {
+        const float *krow = kb + (int64_t)j * k_rs;
+        float s = 0.f;
+#pragma unroll 1
+        for (int d = 0; d < D; ++d) s = __fadd_rn(s, __fmul_rn(qrow[d], krow[d]));
+        const float w = expf(__fmul_rn(s, scale) - mx) / sum;
+        const float *vrow = vb + (int64_t)j * v_rs + d0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (d0 + e < D) o[e] = __fadd_rn(o[e], __fmul_rn(w, vrow[e]));
+    }
+    return make_float4(o[0], o[1], o[2], o[3]);
+}
+
+__device__ __forceinline__ bool finite4(float4 x) {
+    return (fabsf(x.x) <= 3.40282347e38f) & (fabsf(x.y) <= 3.40282347e38f) & (fabsf(x.z) <= 3.40282347e38f) &
+           (fabsf(x.w) <= 3.40282347e38f);
+}
+
 // The split kernel's share of a tile: this wave's subtile t (keys 16t .. 16t + 15)
 // only.  S^T of the subtile against the lane's Q slice, register r of lane
 // (g, li) the raw score of key 16t + 4r + g.
@@ -617,7 +670,7 @@ __device__ __forceinline__ void lap(StageClock *c, uint64_t &bucket) {
 // is loaded into registers before the first is computed, so the tile loads' latencies
 // overlap each other rather than each one the previous tile's arithmetic.
 template <int DP, bool FUSED, bool TIMED, bool SKIP = false, bool SPLIT = false, int MK = -1,
-          bool SINGLE = false, int MAXT = 0>  // head_dim padded to a multiple of 16
+          bool SINGLE = false, int MAXT = 0, bool EXACTV = true>  // head_dim padded to a multiple of 16
 __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, float *__restrict__ ks,
                                             float *__restrict__ vs, StageClock *clk) {
     static_assert(!FUSED || DP == 64, "the fused issue is written for head_dim 64");
@@ -642,6 +695,10 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
     const int D = a.head_dim;
     const int dch = D / 4;  // valid chunks per row
     const int kind = MK >= 0 ? MK : a.mask_kind, arg = a.mask_arg;
+    // Key ranges that differ between the rows of a 16-row wave (see exact_chunk).
+    // (EXACTV false: the launch has checked that the mask has no such ranges.)
+    const bool ragged = EXACTV && (kind == RAYA_MASK_WINDOW64 || kind == RAYA_MASK_SLIDING ||
+                                   (kind == RAYA_MASK_BLOCKDIAG && arg % 16 != 0));
     // exp(scale * (x - y)) = exp2((x - y) * c) on raw dot products x, y; a
     // negative scale is carried by negating Q, so c > 0 and max commutes.  c is
     // kept at least FLT_MIN so that a masked key (x = -inf) weighs exactly 0
@@ -1057,7 +1114,11 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                         for (int w = 0; w < kWaves; ++w) acc += sw[w] * ks[((w * NT + n) * 4 + r) * 64 + lane];
                         e4[e] = zero_row ? 0.f : acc * inv;
                     }
-                    *(float4 *)(orow + 4 * c) = make_float4(e4[0], e4[1], e4[2], e4[3]);
+                    float4 y = make_float4(e4[0], e4[1], e4[2], e4[3]);
+                    if (ragged && !zero_row && !finite4(y))
+                        y = exact_chunk(a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qi * a.q_rs, kb, a.k_rs, vb,
+                                        a.v_rs, rr.lo, rr.hi, D, a.scale, g * DQ + 4 * c);
+                    *(float4 *)(orow + 4 * c) = y;
                 }
             }
         }
@@ -1081,6 +1142,7 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
         float *st = ks + wave * 16 * 64;
         const bool zero_row = qi >= valid || l == 0.f;
         const float inv = zero_row ? 0.f : 1.f / l;
+        bool bad = false;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1090,7 +1152,18 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                 y.z = oacc[2][c] * inv;
                 y.w = oacc[3][c] * inv;
             }
+            bad |= !zero_row && !finite4(y);
             *(float4 *)(st + li * 64 + 4 * ((4 * g + c) ^ li)) = y;
+        }
+        // Non-finite chunks under ragged masks are recomputed (exact_chunk) in place.
+        if (ragged && __any(bad)) {
+#pragma unroll 1
+            for (int c = 0; c < 4; ++c) {
+                float4 *slot = (float4 *)(st + li * 64 + 4 * ((4 * g + c) ^ li));
+                if (!zero_row && !finite4(*slot))
+                    *slot = exact_chunk(a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qi * a.q_rs, kb, a.k_rs, vb,
+                                        a.v_rs, rr.lo, rr.hi, D, a.scale, 16 * g + 4 * c);
+            }
         }
         // One wave's LDS accesses complete in order: the reads see the writes.
         const int rows = packed ? valid : a.seq;
@@ -1116,17 +1189,20 @@ __device__ __forceinline__ void attend_body(const AttnLaunch &a, const Plan &p, 
                     y.z = oacc[(4 * c + 2) % NT][(4 * c + 2) / NT] * inv;
                     y.w = oacc[(4 * c + 3) % NT][(4 * c + 3) / NT] * inv;
                 }
+                if (ragged && !zero_row && !finite4(y))
+                    y = exact_chunk(a.q + base(a.q_bs, a.q_hs, a.q_rs) + (int64_t)qi * a.q_rs, kb, a.k_rs, vb,
+                                    a.v_rs, rr.lo, rr.hi, D, a.scale, g * DQ + 4 * c);
                 *(float4 *)(orow + 4 * c) = y;
             }
         }
     }
 }
 
-template <int DP, bool FUSED>
+template <int DP, bool FUSED, bool EXACTV>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, FUSED, false>(a, p, ks, vs, nullptr);
+    attend_body<DP, FUSED, false, false, false, -1, false, 0, EXACTV>(a, p, ks, vs, nullptr);
 }
 
 // Head_dim 64 under Window64 and Sliding(w): the fused kernel with subtile
@@ -1144,7 +1220,8 @@ template <int DP, bool SKIP>
 __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_blockdiag_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, true, false, SKIP, false, RAYA_MASK_BLOCKDIAG, true>(a, p, ks, vs, nullptr);
+    // BlockDiag(64) rows of a wave share one range; narrower blocks may not.
+    attend_body<DP, true, false, SKIP, false, RAYA_MASK_BLOCKDIAG, true, 0, SKIP>(a, p, ks, vs, nullptr);
 }
 
 template <int DP, int MK>
@@ -1156,23 +1233,23 @@ __global__ void __launch_bounds__(kThreads, kMinWaves<DP>) attend_sliding_kernel
 
 // 16-row items with the key tiles split over the four waves, for grids that
 // leave most compute units idle with 64-row items.
-template <int DP, bool FUSED, int MK = -1, bool SINGLE = false>
+template <int DP, bool FUSED, int MK = -1, bool SINGLE = false, bool EXACTV = true>
 __global__ void __launch_bounds__(kThreads, (kMinWavesOf<DP, true, FUSED>)) attend_split_kernel(const AttnLaunch a,
                                                                                                const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * DP];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * DP];
-    attend_body<DP, FUSED, false, false, true, MK, SINGLE>(a, p, ks, vs, nullptr);
+    attend_body<DP, FUSED, false, false, true, MK, SINGLE, 0, EXACTV>(a, p, ks, vs, nullptr);
 }
 
 // The split kernel at head_dim 64 for items of at most MAXT tiles, every tile's K/V
 // loads issued before the first tile is computed.  2 waves per SIMD hold the MAXT
 // register sets (239 VGPRs at MAXT = 6); the small grids this kernel serves place at
 // most two workgroups per compute unit.
-template <int MAXT>
+template <int MAXT, bool EXACTV>
 __global__ void __launch_bounds__(kThreads, 2) attend_split_all_kernel(const AttnLaunch a, const Plan p) {
     __shared__ __attribute__((aligned(16))) float ks[kKeys * 64];
     __shared__ __attribute__((aligned(16))) float vs[kKeys * 64];
-    attend_body<64, true, false, false, true, -1, false, MAXT>(a, p, ks, vs, nullptr);
+    attend_body<64, true, false, false, true, -1, false, MAXT, EXACTV>(a, p, ks, vs, nullptr);
 }
 
 // The same kernel with the stage clock.  Per-wave totals are summed in LDS,
@@ -1283,6 +1360,18 @@ int rotate_shift(const AttnLaunch &a) {
     return a.mask_kind == RAYA_MASK_BLOCK3 || wide_block ? 2 : -1;
 }
 
+template <bool EXACTV>
+void launch_split_all(int64_t t, dim3 grid, dim3 block, hipStream_t stream, const AttnLaunch &a, const Plan &p) {
+    if (t <= 2)
+        hipLaunchKernelGGL((attend_split_all_kernel<2, EXACTV>), grid, block, 0, stream, a, p);
+    else if (t <= 3)
+        hipLaunchKernelGGL((attend_split_all_kernel<3, EXACTV>), grid, block, 0, stream, a, p);
+    else if (t <= 4)
+        hipLaunchKernelGGL((attend_split_all_kernel<4, EXACTV>), grid, block, 0, stream, a, p);
+    else
+        hipLaunchKernelGGL((attend_split_all_kernel<6, EXACTV>), grid, block, 0, stream, a, p);
+}
+
 template <int DP, bool FUSED = false>
 hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     const bool split = use_split(a);
@@ -1314,25 +1403,29 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
     }
     const dim3 grid((unsigned)total), block(kThreads);
     const bool sliding = a.mask_kind == RAYA_MASK_SLIDING || a.mask_kind == RAYA_MASK_WINDOW64;
+    // Masks whose key ranges differ between the 16 rows of a wave take the kernels
+    // that recompute non-finite output chunks (exact_chunk).
+    const bool ragged = sliding || (a.mask_kind == RAYA_MASK_BLOCKDIAG && a.mask_arg % 16 != 0);
     if (split) {
         if (a.stage_cycles)
             hipLaunchKernelGGL((attend_timed_kernel<DP, FUSED, false, true>), grid, block, 0, stream, a, p);
         else if (FUSED && a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
-            hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, RAYA_MASK_BLOCKDIAG, true>), grid, block, 0, stream, a, p);
+            if (a.mask_arg < 16)
+                hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, RAYA_MASK_BLOCKDIAG, true, true>), grid, block, 0, stream, a, p);
+            else
+                hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, RAYA_MASK_BLOCKDIAG, true, false>), grid, block, 0, stream, a, p);
         else if (FUSED && prefetch_all() && max_item_tiles(a) >= 2 && max_item_tiles(a) <= 6) {
             // (Single-tile items have no later load to overlap.)
             const int64_t t = max_item_tiles(a);
-            if (t <= 2)
-                hipLaunchKernelGGL((attend_split_all_kernel<2>), grid, block, 0, stream, a, p);
-            else if (t <= 3)
-                hipLaunchKernelGGL((attend_split_all_kernel<3>), grid, block, 0, stream, a, p);
-            else if (t <= 4)
-                hipLaunchKernelGGL((attend_split_all_kernel<4>), grid, block, 0, stream, a, p);
+            if (ragged)
+                launch_split_all<true>(t, grid, block, stream, a, p);
             else
-                hipLaunchKernelGGL((attend_split_all_kernel<6>), grid, block, 0, stream, a, p);
+                launch_split_all<false>(t, grid, block, stream, a, p);
         }
+        else if (ragged)
+            hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, -1, false, true>), grid, block, 0, stream, a, p);
         else
-            hipLaunchKernelGGL((attend_split_kernel<DP, FUSED>), grid, block, 0, stream, a, p);
+            hipLaunchKernelGGL((attend_split_kernel<DP, FUSED, -1, false, false>), grid, block, 0, stream, a, p);
         return hipGetLastError();
     }
     if constexpr (FUSED) {
@@ -1348,13 +1441,17 @@ hipError_t launch_dp(const AttnLaunch &a, hipStream_t stream) {
             hipLaunchKernelGGL((attend_blockdiag_kernel<DP, false>), grid, block, 0, stream, a, p);
         else if (a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg == 0)
             hipLaunchKernelGGL((attend_blockdiag_kernel<DP, true>), grid, block, 0, stream, a, p);
+        else if (ragged)
+            hipLaunchKernelGGL((attend_kernel<DP, true, true>), grid, block, 0, stream, a, p);
         else
-            hipLaunchKernelGGL((attend_kernel<DP, true>), grid, block, 0, stream, a, p);
+            hipLaunchKernelGGL((attend_kernel<DP, true, false>), grid, block, 0, stream, a, p);
     } else {
         if (a.stage_cycles)
             hipLaunchKernelGGL((attend_timed_kernel<DP, false, false>), grid, block, 0, stream, a, p);
+        else if (ragged)
+            hipLaunchKernelGGL((attend_kernel<DP, false, true>), grid, block, 0, stream, a, p);
         else
-            hipLaunchKernelGGL((attend_kernel<DP, false>), grid, block, 0, stream, a, p);
+            hipLaunchKernelGGL((attend_kernel<DP, false, false>), grid, block, 0, stream, a, p);
     }
     return hipGetLastError();
 }

@@ -602,33 +602,36 @@ def test_row_strides_past_the_fused_offset_range(hip_attention):
         check_close(got, want[0, 0], name)
 
 
-def test_non_finite_v_outside_a_window(hip_attention):
-    """An Inf in V at key j (dim c) under Window64.  The reference sums over each row's own
-    key range only (naive.rs:13-65), so rows whose window holds j get Inf in dim c and every
-    other row stays finite.  Here the PV product runs over whole 16-key subtiles on the
-    matrix core, so a row whose window excludes j but whose workgroup's subtiles include it
-    gets 0 x Inf = NaN in dim c (and only there).  Pinned: rows with j in their window are
-    +Inf in dim c and match the oracle elsewhere; every other row matches the oracle in every
-    dim but c, where it is the oracle's value or NaN; padded rows are exact zeros."""
-    h, s, d, valid, j, c = 2, 512, 64, 400, 200, 5
-    q, k, v = oracle.qkv(h, s, d, 77)
-    v = v.copy()
-    v[:, j, c] = np.inf
-    for mask, okind in ((R.Mask.WINDOW64, oracle.MASK_WINDOW64), (R.Mask.sliding(64), oracle.MASK_SLIDING)):
-        got = run_hip(hip_attention, q, k, v, mask, valid, fill=np.nan)
-        want = oracle_naive(q, k, v, okind, valid, 128, 64)
-        assert (got[:, valid:] == 0).all(), "padded rows must be literal zeros"
-        sees = np.abs(np.arange(valid) - j) <= 64
-        others = [x for x in range(d) if x != c]
-        assert (got[:, :valid][:, sees, c] == np.inf).all()
-        assert (want[:, :valid][:, sees, c] == np.inf).all()
-        check_close(got[:, :valid][..., others], want[:, :valid][..., others], mask.name())
-        gc, wc = got[:, :valid][:, ~sees, c], want[:, :valid][:, ~sees, c]
-        assert np.isfinite(wc).all()
-        same = np.isfinite(gc)
-        assert (np.isnan(gc) | same).all()
-        assert np.abs(gc[same] - wc[same]).max() < MAX_ABS
-        print(f"{mask.name()}: {int((~same).sum())} of {gc.size} rows outside the window are NaN in dim {c}")
+@pytest.mark.parametrize("d", [64, 40])
+@pytest.mark.parametrize("name", ["window64", "sliding64", "sliding8", "block_diag8", "block_diag24"])
+def test_non_finite_v_outside_a_window(hip_attention, name, d):
+    """An Inf or NaN in V at key j, dim c, under masks whose rows' key ranges differ within a
+    16-row wave.  The reference sums each row over its own key range only (naive.rs:13-65), so
+    rows whose range holds j are +Inf / -Inf / NaN in dim c and every other output is finite.
+    The kernels find such a value in a 16-key subtile cut by some row's range and compute that
+    subtile's PV key by key over each row's own range, so the results match the reference's
+    pattern exactly (a key outside a row's range never meets its zero weight).  Keys at the
+    start, middle and end of a subtile; head_dim 64 (the fused kernels) and 40 (the general
+    ones)."""
+    masks = dict(MASKS)
+    masks["block_diag8"] = (R.Mask.block_diag(8), oracle.MASK_BLOCKDIAG, 8, 0)
+    masks["block_diag24"] = (R.Mask.block_diag(24), oracle.MASK_BLOCKDIAG, 24, 0)
+    mask, okind, block, window = masks[name]
+    h, s_, valid, c = 2, 512, 400, 5
+    q, k, v = oracle.qkv(h, s_, d, 77)
+    for j in (200, 207, 255, 399):
+        for bad in (np.inf, -np.inf, np.nan):
+            vv = v.copy()
+            vv[:, j, c] = bad
+            got = run_hip(hip_attention, q, k, vv, mask, valid, fill=np.nan)
+            want = oracle_naive(q, k, vv, okind, valid, block, window)
+            assert (got[:, valid:] == 0).all(), "padded rows must be literal zeros"
+            g, w = got[:, :valid], want[:, :valid]
+            assert (~np.isfinite(w)).any()
+            assert (np.isnan(g) == np.isnan(w)).all(), (name, j, bad)
+            assert (np.isinf(g) == np.isinf(w)).all() and (g[np.isinf(w)] == w[np.isinf(w)]).all(), (name, j, bad)
+            fin = np.isfinite(w)
+            assert np.abs(g[fin] - w[fin]).max() < MAX_ABS, (name, j, bad)
 
 
 @pytest.mark.parametrize("d", [64, 40, 128])
