@@ -1340,14 +1340,16 @@ bool prefetch_all() {
 // pair's index, gives every XCD an equal share of every pair while a unit's
 // items still share their key tiles in one L2: the MFMA-bound multi-tile lines
 // gain about 1% (Block3 and BlockDiag(128) at 4 x 12 x 16384, Block3 at 32 x
-// 12 x 2048).  Single-tile BlockDiag(b <= 64) keeps whole pairs: HBM-bound, it
-// runs the same either way (the XCD that finishes early leaves its bandwidth
-// to the others), and units of 1 or 2 tiles, which scatter neighbouring rows
-// over the XCDs, run it 16-20% slower.  Window64 and Sliding keep whole pairs
-// too (units of 4 tiles: 0.4-1.5% slower on 16 heads x 4096 and 8192 rows).  RAYA_ATTN_ORDER=pairs keeps whole
-// pairs, rot1/rot2/rot4/rot8 deal units of that many tiles for any mask; the
-// units must divide a pair's tiles 8 times over, else whole pairs.  Returns
-// the shift, or -1 for whole pairs.
+// 12 x 2048).  A batch of one sequence gives every pair the same valid length
+// and keeps whole pairs (16 heads x 2048 rows under Block3 ran 1% slower in
+// units).  Single-tile BlockDiag(b <= 64) keeps whole pairs: HBM-bound, it runs
+// the same either way (the XCD that finishes early leaves its bandwidth to the
+// others), and units of 1 or 2 tiles, which scatter neighbouring rows over the
+// XCDs, run it 16-20% slower.  Window64 and Sliding keep whole pairs too (units
+// of 4 tiles: 0.4-1.5% slower on 16 heads x 4096 and 8192 rows).
+// RAYA_ATTN_ORDER=pairs keeps whole pairs, rot1/rot2/rot4/rot8 deal units of
+// that many tiles for any mask; the units must divide a pair's tiles 8 times
+// over, else whole pairs.  Returns the shift, or -1 for whole pairs.
 int rotate_shift(const AttnLaunch &a) {
     if (const char *e = std::getenv("RAYA_ATTN_ORDER")) {
         if (!std::strcmp(e, "pairs")) return -1;
@@ -1357,7 +1359,8 @@ int rotate_shift(const AttnLaunch &a) {
         if (!std::strcmp(e, "rot8")) return 3;
     }
     const bool wide_block = a.mask_kind == RAYA_MASK_BLOCKDIAG && kKeys % a.mask_arg != 0;
-    return a.mask_kind == RAYA_MASK_BLOCK3 || wide_block ? 2 : -1;
+    // One sequence gives every pair the same valid length: whole pairs are balanced.
+    return (a.mask_kind == RAYA_MASK_BLOCK3 || wide_block) && a.batch > 1 ? 2 : -1;
 }
 
 template <bool EXACTV>
