@@ -602,7 +602,7 @@ def test_row_strides_past_the_fused_offset_range(hip_attention):
         check_close(got, want[0, 0], name)
 
 
-@pytest.mark.parametrize("d", [64, 40])
+@pytest.mark.parametrize("d", [64, 40, 136])
 @pytest.mark.parametrize("name", ["window64", "sliding64", "sliding8", "block_diag8", "block_diag24"])
 def test_non_finite_v_outside_a_window(hip_attention, name, d):
     """An Inf or NaN in V at key j, dim c, under masks whose rows' key ranges differ within a
@@ -611,8 +611,8 @@ def test_non_finite_v_outside_a_window(hip_attention, name, d):
     The kernels find such a value in a 16-key subtile cut by some row's range and compute that
     subtile's PV key by key over each row's own range, so the results match the reference's
     pattern exactly (a key outside a row's range never meets its zero weight).  Keys at the
-    start, middle and end of a subtile; head_dim 64 (the fused kernels) and 40 (the general
-    ones)."""
+    start, middle and end of a subtile; head_dim 64 (the fused kernels), 40 and 136 (the general
+    ones, 136 padded to 160)."""
     masks = dict(MASKS)
     masks["block_diag8"] = (R.Mask.block_diag(8), oracle.MASK_BLOCKDIAG, 8, 0)
     masks["block_diag24"] = (R.Mask.block_diag(24), oracle.MASK_BLOCKDIAG, 24, 0)
