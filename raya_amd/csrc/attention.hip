@@ -456,9 +456,8 @@ __device__ __forceinline__ void pv_tile(const float *vs, const floatx4 (&sacc)[4
 // (the path only runs on non-finite inputs).  Scores are the dot product in dim
 // order times the scale; the maximum ignores NaN scores as the reference's
 // f32::max does, and a NaN or +Inf score makes the row NaN through the sum.
-__device__ __forceinline__ float4 exact_chunk(const float *qrow, const float *kb, int64_t k_rs,
-                                                        const float *vb, int64_t v_rs, int lo, int hi, int D,
-                                                        float scale, int d0) {
+__device__ __forceinline__ float4 exact_chunk(const float *qrow, const float *kb, int64_t k_rs, const float *vb,
+                                              int64_t v_rs, int lo, int hi, int D, float scale, int d0) {
     float mx = -INFINITY;
 #pragma unroll 1
     for (int j = lo; j < hi; ++j) {
